@@ -1,0 +1,60 @@
+"""Build the gfx950 shared library ``ternel_amd/_lib/libternel_tq1.so`` in-tree.
+
+``python -m ternel_amd.build`` (or ``__graft_entry__.build()``) cross-compiles
+on a machine without a GPU; the built library travels with the tree.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+REPO_ROOT = PACKAGE_DIR.parent
+SOURCE = PACKAGE_DIR / "csrc" / "tq1_engine.hip"
+INCLUDE_DIR = REPO_ROOT / "include"
+LIB_DIR = PACKAGE_DIR / "_lib"
+LIB_PATH = LIB_DIR / "libternel_tq1.so"
+ARCH = "gfx950"
+
+# Packed fp32 instructions are disabled for every HIP translation unit: some of
+# their forms have given silently wrong results on these machines.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists():
+        raise RuntimeError("hipcc not found; the TQ1 engine needs ROCm's hipcc to build")
+    return found
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the library (always recompiles) and return its path."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", str(SOURCE), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    env = dict(os.environ)
+    result = subprocess.run(cmd, capture_output=True, text=True, env=env)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({result.returncode}):\n{result.stdout}\n{result.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

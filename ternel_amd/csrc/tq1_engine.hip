@@ -1,0 +1,845 @@
+// tq1_engine.hip -- TQ1_G128 packed-weight kernels for MI355X (gfx950, CDNA4).
+//
+// One shared library, C ABI only (include/ternel_tq1.h). All kernels read the
+// canonical 28-byte blocks straight from HBM; nothing model-sized is ever
+// expanded. Kernels:
+//   validate_kernel   fail-closed byte scan (regular > 242, tail > 26)
+//   decode_kernel     bit-exact trit decode (test / inspection entry)
+//   lut_matmul_kernel LUT23 product for M = 1 (decode GEMV) and small batches
+//   mfma_gemm_kernel  trits -> fp16 LDS tiles -> v_mfma_f32_32x32x16_f16
+//   get_rows_kernel   packed embedding-row gather
+// plus an ordered split-K reduction and small helpers.
+
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "ternel_tq1.h"
+
+// ---------------------------------------------------------------------------
+// Format constants (src/bonsai_tq1/format.py:14-24, lut23_reorder.py:27-29)
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kBlockWeights = 128;
+constexpr int kBlockBytes = 28;
+constexpr int kBlockWords = 7;
+constexpr int kCodeSlots = 26;
+constexpr int kFullSlots = 25;
+constexpr uint32_t kMaxTailByte = 26;
+
+// LUT23 tables of one 128-weight group, fp32: L2[25][9] over trits (0,1) of a
+// slot, L3[25][27] over trits (2,3,4), tail[27] over trits 125..127.
+constexpr int kL2Entries = 9;
+constexpr int kL3Entries = 27;
+constexpr int kL3Base = kFullSlots * kL2Entries;             // 225
+constexpr int kTailBase = kL3Base + kFullSlots * kL3Entries;  // 900
+constexpr int kLutFloats = kTailBase + 27;                    // 927
+
+constexpr int kThreads = 256;
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define TQ1_HIP_CHECK(expr)                                                                   \
+    do {                                                                                      \
+        hipError_t err_ = (expr);                                                             \
+        if (err_ != hipSuccess)                                                               \
+            return fail(TERNEL_TQ1_EHIP, "%s failed: %s", #expr, hipGetErrorString(err_));    \
+    } while (0)
+
+#define TQ1_LAUNCH_CHECK()                                                                    \
+    do {                                                                                      \
+        hipError_t err_ = hipGetLastError();                                                  \
+        if (err_ != hipSuccess)                                                               \
+            return fail(TERNEL_TQ1_EHIP, "kernel launch failed: %s", hipGetErrorString(err_)); \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Scalar conversions. fp16 via _Float16 (v_cvt_f32_f16 keeps subnormals, inf
+// and NaN); bf16 by bit manipulation with round-to-nearest-even.
+// ---------------------------------------------------------------------------
+struct bf16_t {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    const uint16_t b = static_cast<uint16_t>(bits);
+    _Float16 h;
+    __builtin_memcpy(&h, &b, sizeof(h));
+    return static_cast<float>(h);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v);
+template <>
+__device__ __forceinline__ float to_f32<_Float16>(_Float16 v) {
+    return static_cast<float>(v);
+}
+template <>
+__device__ __forceinline__ float to_f32<bf16_t>(bf16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) {
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) {
+    return static_cast<_Float16>(v);
+}
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+    uint32_t u = __float_as_uint(v);
+    bf16_t out;
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        out.bits = static_cast<uint16_t>((u >> 16) | 0x0040u);  // quiet NaN, sign kept
+    } else {
+        u += 0x7fffu + ((u >> 16) & 1u);
+        out.bits = static_cast<uint16_t>(u >> 16);
+    }
+    return out;
+}
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) {
+    return v;
+}
+
+__device__ __forceinline__ uint32_t block_byte(const uint32_t (&w)[kBlockWords], int index) {
+    return (w[index >> 2] >> ((index & 3) * 8)) & 0xffu;
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Helpers
+// ---------------------------------------------------------------------------
+__global__ void zero_u64_kernel(unsigned long long *p, int n) {
+    const int i = threadIdx.x;
+    if (i < n) p[i] = 0ull;
+}
+
+// ---------------------------------------------------------------------------
+// validate_kernel: counts regular code bytes > 242 and tail bytes > 26.
+// The buffer is walked as 32-bit words; word j (0..6) of a block holds
+//   j = 0: scale, scale, code0, code1      j = 1..5: four codes
+//   j = 6: code22, code23, code24, tail.
+// SWAR per byte b:  b >= 243  <=>  bit7(b) & bit7((b & 0x7f) + 13)
+//                   b >= 27   <=>  bit7(b) | bit7((b & 0x7f) + 101)
+// (the additions never carry across bytes).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void validate_kernel(const uint32_t *__restrict__ words,
+                                                            int64_t nwords,
+                                                            unsigned long long *counters) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    int j = static_cast<int>(first % kBlockWords);
+    const int step = static_cast<int>(stride % kBlockWords);
+    uint32_t bad_regular = 0, bad_tail = 0;
+    for (int64_t w = first; w < nwords; w += stride) {
+        const uint32_t d = words[w];
+        const uint32_t regular_mask = j == 0 ? 0x80800000u : (j == 6 ? 0x00808080u : 0x80808080u);
+        const uint32_t tail_mask = j == 6 ? 0x80000000u : 0u;
+        const uint32_t low7 = d & 0x7f7f7f7fu;
+        bad_regular += __popc(d & (low7 + 0x0d0d0d0du) & regular_mask);
+        bad_tail += __popc((d | (low7 + 0x65656565u)) & tail_mask);
+        j += step;
+        if (j >= kBlockWords) j -= kBlockWords;
+    }
+    bad_regular = wave_sum_u32(bad_regular);
+    bad_tail = wave_sum_u32(bad_tail);
+    if ((threadIdx.x & 63) == 0) {
+        if (bad_regular) atomicAdd(&counters[0], static_cast<unsigned long long>(bad_regular));
+        if (bad_tail) atomicAdd(&counters[1], static_cast<unsigned long long>(bad_tail));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// decode_kernel: one thread per (block, code slot); trit i of a byte is
+// (b / 3^i) % 3, exactly as src/bonsai_tq1/format.py:112-121 computes it.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void decode_kernel(const uint8_t *__restrict__ blocks,
+                                                          int64_t nblocks,
+                                                          uint8_t *__restrict__ scales_out,
+                                                          uint8_t *__restrict__ codes_out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= nblocks * kCodeSlots) return;
+    const int64_t n = i / kCodeSlots;
+    const int s = static_cast<int>(i - n * kCodeSlots);
+    const uint8_t *blk = blocks + n * kBlockBytes;
+    const uint32_t b = blk[2 + s];
+    uint8_t *codes = codes_out + n * kBlockWeights;
+    if (s < kFullSlots) {
+        codes[5 * s + 0] = static_cast<uint8_t>(b % 3u);
+        codes[5 * s + 1] = static_cast<uint8_t>((b / 3u) % 3u);
+        codes[5 * s + 2] = static_cast<uint8_t>((b / 9u) % 3u);
+        codes[5 * s + 3] = static_cast<uint8_t>((b / 27u) % 3u);
+        codes[5 * s + 4] = static_cast<uint8_t>((b / 81u) % 3u);
+    } else {
+        codes[125] = static_cast<uint8_t>(b % 3u);
+        codes[126] = static_cast<uint8_t>((b / 3u) % 3u);
+        codes[127] = static_cast<uint8_t>((b / 9u) % 3u);
+        scales_out[n * 2 + 0] = blk[0];
+        scales_out[n * 2 + 1] = blk[1];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// get_rows_kernel: one thread per (token, group, code slot) writes the 5 (or
+// 3) weights that byte holds: (t - 1) * scale, evaluated in fp32 and rounded
+// to T (exact for fp16 and fp32). Ids outside [0, rows) give zeros
+// (src/ternel_mlx/kernels.py:869-880).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint8_t *__restrict__ blocks,
+                                                            int64_t rows, int G,
+                                                            const int64_t *__restrict__ ids,
+                                                            int64_t n_ids, T *__restrict__ out) {
+    const int per_token = G * kCodeSlots;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= per_token) return;
+    const int g = i / kCodeSlots;
+    const int s = i - g * kCodeSlots;
+    const int first = s < kFullSlots ? 5 * s : 125;
+    const int count = s < kFullSlots ? 5 : 3;
+    for (int64_t t = blockIdx.y; t < n_ids; t += gridDim.y) {
+        const int64_t id = ids[t];
+        T *o = out + t * static_cast<int64_t>(G) * kBlockWeights + g * kBlockWeights + first;
+        if (id < 0 || id >= rows) {
+            for (int d = 0; d < count; ++d) o[d] = from_f32<T>(0.0f);
+            continue;
+        }
+        const uint8_t *blk = blocks + (id * G + g) * kBlockBytes;
+        const float scale = half_bits_to_float(static_cast<uint32_t>(blk[0]) |
+                                               (static_cast<uint32_t>(blk[1]) << 8));
+        uint32_t b = blk[2 + s];
+        for (int d = 0; d < count; ++d) {
+            const uint32_t q = b / 3u;
+            const uint32_t trit = b - 3u * q;
+            b = q;
+            o[d] = from_f32<T>((static_cast<float>(trit) - 1.0f) * scale);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// lut_matmul_kernel: LUT23 product (the algorithm of src/ternel_mlx/kernels.py
+// :244-342, re-designed for wave64 and canonical blocks).
+//
+// Grid (row tiles of 256, batch tiles of BT, K chunks). A workgroup builds the
+// LUT23 tables of up to `sub_groups` groups x BT activation vectors in LDS,
+// then each lane streams its own row's 28-byte blocks for those groups (seven
+// dword loads, one block of prefetch) and, per code byte p, adds
+// L2[s][p % 9] + L3[s][p / 9] (hi = (p * 57) >> 9, lo = p - 9 hi). All lanes of
+// a wave index the same slot's 9- or 27-entry table, which sit in distinct LDS
+// banks, so the lookups are conflict-free. Per group: acc = fma(scale, sum, acc)
+// with the raw fp16 scale, the summation order of the reference kernel.
+// With more than one K chunk the fp32 partials go to `partial` and
+// reduce_partials_kernel adds them in chunk order (deterministic).
+// Illegal regular bytes stay inside the group's 927-entry table; the tail index
+// is clamped, so no input reads outside the tables.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float lut_entry(const T *__restrict__ xg, int idx) {
+    if (idx < kL3Base) {
+        const int s = idx / kL2Entries;
+        const int c = idx - s * kL2Entries;
+        const float x0 = to_f32<T>(xg[5 * s]);
+        const float x1 = to_f32<T>(xg[5 * s + 1]);
+        return (static_cast<float>(c % 3) - 1.0f) * x0 + (static_cast<float>(c / 3) - 1.0f) * x1;
+    }
+    if (idx < kTailBase) {
+        const int e = idx - kL3Base;
+        const int s = e / kL3Entries;
+        const int c = e - s * kL3Entries;
+        const float x2 = to_f32<T>(xg[5 * s + 2]);
+        const float x3 = to_f32<T>(xg[5 * s + 3]);
+        const float x4 = to_f32<T>(xg[5 * s + 4]);
+        return (static_cast<float>(c % 3) - 1.0f) * x2 +
+               (static_cast<float>((c / 3) % 3) - 1.0f) * x3 +
+               (static_cast<float>(c / 9) - 1.0f) * x4;
+    }
+    const int c = idx - kTailBase;
+    const float x0 = to_f32<T>(xg[125]);
+    const float x1 = to_f32<T>(xg[126]);
+    const float x2 = to_f32<T>(xg[127]);
+    return (static_cast<float>(c % 3) - 1.0f) * x0 +
+           (static_cast<float>((c / 3) % 3) - 1.0f) * x1 +
+           (static_cast<float>(c / 9) - 1.0f) * x2;
+}
+
+template <typename T, int BT>
+__global__ __launch_bounds__(kThreads) void lut_matmul_kernel(
+    const uint8_t *__restrict__ blocks, const T *__restrict__ x, T *__restrict__ y,
+    float *__restrict__ partial, int M, int N, int G, int chunk_groups, int sub_groups) {
+    extern __shared__ float lut[];
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x * kThreads + tid;
+    const int batch0 = blockIdx.y * BT;
+    const int chunk = blockIdx.z;
+    const int g_begin = chunk * chunk_groups;
+    const int g_end = min(G, g_begin + chunk_groups);
+    const int64_t K = static_cast<int64_t>(G) * kBlockWeights;
+    const uint32_t *row_words =
+        reinterpret_cast<const uint32_t *>(blocks) + static_cast<int64_t>(row) * G * kBlockWords;
+
+    float acc[BT];
+#pragma unroll
+    for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
+
+    for (int g0 = g_begin; g0 < g_end; g0 += sub_groups) {
+        const int ng = min(sub_groups, g_end - g0);
+        __syncthreads();  // previous tables fully consumed
+        const int per_vector = ng * kLutFloats;
+        for (int e = tid; e < BT * per_vector; e += kThreads) {
+            const int j = e / per_vector;
+            const int rem = e - j * per_vector;
+            const int gi = rem / kLutFloats;
+            const int idx = rem - gi * kLutFloats;
+            const int sample = min(batch0 + j, M - 1);
+            const T *xg = x + static_cast<int64_t>(sample) * K +
+                          static_cast<int64_t>(g0 + gi) * kBlockWeights;
+            lut[(j * sub_groups + gi) * kLutFloats + idx] = lut_entry<T>(xg, idx);
+        }
+        __syncthreads();
+        if (row < N) {
+            uint32_t w[kBlockWords], nw[kBlockWords];
+            const uint32_t *bp = row_words + static_cast<int64_t>(g0) * kBlockWords;
+#pragma unroll
+            for (int k = 0; k < kBlockWords; ++k) w[k] = bp[k];
+            for (int gi = 0; gi < ng; ++gi) {
+                if (gi + 1 < ng) {
+#pragma unroll
+                    for (int k = 0; k < kBlockWords; ++k) nw[k] = bp[(gi + 1) * kBlockWords + k];
+                }
+                const float scale = half_bits_to_float(w[0]);
+                float sum[BT];
+#pragma unroll
+                for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
+#pragma unroll
+                for (int s = 0; s < kFullSlots; ++s) {
+                    const uint32_t p = block_byte(w, 2 + s);
+                    const uint32_t hi = (p * 57u) >> 9;
+                    const uint32_t lo = p - 9u * hi;
+#pragma unroll
+                    for (int j = 0; j < BT; ++j) {
+                        const float *L = lut + (j * sub_groups + gi) * kLutFloats;
+                        sum[j] += L[s * kL2Entries + lo] + L[kL3Base + s * kL3Entries + hi];
+                    }
+                }
+                const uint32_t tail = min(w[6] >> 24, kMaxTailByte);
+#pragma unroll
+                for (int j = 0; j < BT; ++j) {
+                    sum[j] += lut[(j * sub_groups + gi) * kLutFloats + kTailBase + tail];
+                    acc[j] = fmaf(scale, sum[j], acc[j]);
+                }
+#pragma unroll
+                for (int k = 0; k < kBlockWords; ++k) w[k] = nw[k];
+            }
+        }
+    }
+
+    if (row < N) {
+#pragma unroll
+        for (int j = 0; j < BT; ++j) {
+            const int sample = batch0 + j;
+            if (sample < M) {
+                if (partial)
+                    partial[(static_cast<int64_t>(chunk) * M + sample) * N + row] = acc[j];
+                else
+                    y[static_cast<int64_t>(sample) * N + row] = from_f32<T>(acc[j]);
+            }
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void reduce_partials_kernel(const float *__restrict__ partial,
+                                                                   T *__restrict__ y, int64_t count,
+                                                                   int splits) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float a = partial[i];
+    for (int c = 1; c < splits; ++c) a += partial[static_cast<int64_t>(c) * count + i];
+    y[i] = from_f32<T>(a);
+}
+
+// ---------------------------------------------------------------------------
+// mfma_gemm_kernel: y = x @ W^T on CDNA4 matrix cores.
+//
+// Workgroup tile 128 (M) x 128 (N), one 128-weight group per K step. Each K
+// step stages the activation tile (fp16, straight copy) and decodes the weight
+// tile -- 128 rows x one 28-byte block -- into fp16 (t - 1) * scale in LDS
+// (exact in fp16, so the only rounding is the fp32 accumulation). Four waves
+// in a 2 x 2 grid each own 64 x 64 outputs = 2 x 2 tiles of
+// v_mfma_f32_32x32x16_f16. LDS rows are padded by 8 halves so the 16-byte
+// fragment reads of a wave fall in distinct banks.
+// ---------------------------------------------------------------------------
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+constexpr int kGemmBM = 128;
+constexpr int kGemmBN = 128;
+constexpr int kGemmStride = kBlockWeights + 8;  // halves per LDS row
+
+template <int H>
+__device__ __forceinline__ void decode_half_block(const uint32_t (&w)[kBlockWords], float scale,
+                                                  _Float16 (&out)[64]) {
+#pragma unroll
+    for (int kk = 0; kk < 64; ++kk) {
+        const int k = H * 64 + kk;
+        const int s = k < 125 ? k / 5 : kFullSlots;
+        const int d = k < 125 ? k % 5 : k - 125;
+        const uint32_t b = block_byte(w, 2 + s);
+        const uint32_t p3 = d == 0 ? 1u : d == 1 ? 3u : d == 2 ? 9u : d == 3 ? 27u : 81u;
+        const uint32_t t = (b / p3) % 3u;
+        out[kk] = static_cast<_Float16>((static_cast<float>(t) - 1.0f) * scale);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
+    const uint8_t *__restrict__ blocks, const _Float16 *__restrict__ x, _Float16 *__restrict__ y,
+    float *__restrict__ partial, int M, int N, int G, int chunk_groups) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[kGemmBM * kGemmStride];
+    __shared__ __attribute__((aligned(16))) _Float16 ws[kGemmBN * kGemmStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n0 = blockIdx.x * kGemmBN;
+    const int m0 = blockIdx.y * kGemmBM;
+    const int chunk = blockIdx.z;
+    const int g_begin = chunk * chunk_groups;
+    const int g_end = min(G, g_begin + chunk_groups);
+    const int64_t K = static_cast<int64_t>(G) * kBlockWeights;
+    const int wm = (wave >> 1) * 64;
+    const int wn = (wave & 1) * 64;
+
+    float16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int dec_row = tid >> 1;
+    const int dec_half = tid & 1;
+    const int dec_n = n0 + dec_row;
+
+    for (int g = g_begin; g < g_end; ++g) {
+        // Activation tile: 128 rows x 16 chunks of 8 halves.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = tid + i * kThreads;
+            const int r = idx >> 4;
+            const int c8 = idx & 15;
+            const int m = m0 + r;
+            half8 v;
+            if (m < M) {
+                v = *reinterpret_cast<const half8 *>(x + static_cast<int64_t>(m) * K +
+                                                     static_cast<int64_t>(g) * kBlockWeights + c8 * 8);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = static_cast<_Float16>(0.0f);
+            }
+            *reinterpret_cast<half8 *>(xs + r * kGemmStride + c8 * 8) = v;
+        }
+        // Weight tile: each thread decodes half a block of one row.
+        {
+            _Float16 wv[64];
+            if (dec_n < N) {
+                const uint32_t *bp = reinterpret_cast<const uint32_t *>(blocks) +
+                                     (static_cast<int64_t>(dec_n) * G + g) * kBlockWords;
+                uint32_t w[kBlockWords];
+#pragma unroll
+                for (int k = 0; k < kBlockWords; ++k) w[k] = bp[k];
+                const float scale = half_bits_to_float(w[0]);
+                if (dec_half == 0)
+                    decode_half_block<0>(w, scale, wv);
+                else
+                    decode_half_block<1>(w, scale, wv);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 64; ++e) wv[e] = static_cast<_Float16>(0.0f);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                half8 v;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = wv[q * 8 + e];
+                *reinterpret_cast<half8 *>(ws + dec_row * kGemmStride + dec_half * 64 + q * 8) = v;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kBlockWeights / 16; ++kk) {
+            half8 a[2], b[2];
+            const int kofs = kk * 16 + (lane >> 5) * 8;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const half8 *>(xs + (wm + i * 32 + (lane & 31)) * kGemmStride + kofs);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const half8 *>(ws + (wn + j * 32 + (lane & 31)) * kGemmStride + kofs);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    // D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) % 2), item 4 * (i / 8) + i % 4.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int n = n0 + wn + j * 32 + (lane & 31);
+                if (m < M && n < N) {
+                    if (partial)
+                        partial[(static_cast<int64_t>(chunk) * M + m) * N + n] = acc[i][j][r];
+                    else
+                        y[static_cast<int64_t>(m) * N + n] = static_cast<_Float16>(acc[i][j][r]);
+                }
+            }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side geometry
+// ---------------------------------------------------------------------------
+// Workgroups a split is sized to reach: a few per CU on the 256-CU part.
+constexpr int64_t kSplitTargetWorkgroups = 1024;
+constexpr int kLutMaxBytes = 64 * 1024;
+
+int largest_split(int64_t groups_per_row, int64_t workgroups) {
+    int64_t budget = kSplitTargetWorkgroups / (workgroups > 0 ? workgroups : 1);
+    if (budget < 1) budget = 1;
+    if (budget > groups_per_row) budget = groups_per_row;
+    for (int64_t k = budget; k > 1; --k)
+        if (groups_per_row % k == 0) return static_cast<int>(k);
+    return 1;
+}
+
+int check_dtype(int dtype) {
+    if (dtype != TERNEL_TQ1_F16 && dtype != TERNEL_TQ1_BF16 && dtype != TERNEL_TQ1_F32)
+        return fail(TERNEL_TQ1_EINVAL, "unsupported dtype code %d", dtype);
+    return TERNEL_TQ1_OK;
+}
+
+int check_geometry(int64_t M, int64_t rows, int64_t columns) {
+    if (rows <= 0 || columns <= 0)
+        return fail(TERNEL_TQ1_EINVAL, "tensor dimensions must be positive, got %lldx%lld",
+                    static_cast<long long>(rows), static_cast<long long>(columns));
+    if (columns % kBlockWeights)
+        return fail(TERNEL_TQ1_EINVAL, "%lld columns is not a multiple of the 128-weight group",
+                    static_cast<long long>(columns));
+    if (M <= 0) return fail(TERNEL_TQ1_EINVAL, "activations have an empty batch dimension");
+    if (rows > INT32_MAX || M > INT32_MAX || columns / kBlockWeights > INT32_MAX)
+        return fail(TERNEL_TQ1_EINVAL, "tensor too large for 32-bit row/batch indices");
+    return TERNEL_TQ1_OK;
+}
+
+struct LutPlan {
+    int batch_tile;
+    int k_split;
+    int chunk_groups;
+    int sub_groups;
+    int64_t tiles;
+    int64_t batch_tiles;
+};
+
+int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split, LutPlan *plan) {
+    const int64_t G = columns / kBlockWeights;
+    if (batch_tile == 0) batch_tile = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
+    if (batch_tile != 1 && batch_tile != 2 && batch_tile != 4)
+        return fail(TERNEL_TQ1_EINVAL, "batch tile must be 1, 2 or 4, got %d", batch_tile);
+    plan->batch_tile = batch_tile;
+    plan->tiles = (rows + kThreads - 1) / kThreads;
+    plan->batch_tiles = (M + batch_tile - 1) / batch_tile;
+    if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
+    if (k_split == 0) k_split = largest_split(G, plan->tiles * plan->batch_tiles);
+    if (G % k_split)
+        return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row",
+                    k_split, static_cast<long long>(G));
+    plan->k_split = k_split;
+    plan->chunk_groups = static_cast<int>(G / k_split);
+    const int cap = kLutMaxBytes / (batch_tile * kLutFloats * 4);
+    int sub = plan->chunk_groups;
+    if (sub > cap) {
+        // Equal sub-chunks no larger than the LDS cap.
+        const int pieces = (plan->chunk_groups + cap - 1) / cap;
+        sub = (plan->chunk_groups + pieces - 1) / pieces;
+    }
+    plan->sub_groups = sub;
+    return TERNEL_TQ1_OK;
+}
+
+template <typename T>
+int launch_lut(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows,
+               int64_t columns, const LutPlan &plan, float *partial, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(plan.tiles), static_cast<unsigned>(plan.batch_tiles),
+                    static_cast<unsigned>(plan.k_split));
+    const size_t lds = static_cast<size_t>(plan.batch_tile) * plan.sub_groups * kLutFloats * 4;
+    const int G = static_cast<int>(columns / kBlockWeights);
+    const T *xt = static_cast<const T *>(x);
+    T *yt = static_cast<T *>(y);
+    switch (plan.batch_tile) {
+        case 1:
+            hipLaunchKernelGGL((lut_matmul_kernel<T, 1>), grid, dim3(kThreads), lds, stream, blocks, xt, yt,
+                               partial, static_cast<int>(M), static_cast<int>(rows), G,
+                               plan.chunk_groups, plan.sub_groups);
+            break;
+        case 2:
+            hipLaunchKernelGGL((lut_matmul_kernel<T, 2>), grid, dim3(kThreads), lds, stream, blocks, xt, yt,
+                               partial, static_cast<int>(M), static_cast<int>(rows), G,
+                               plan.chunk_groups, plan.sub_groups);
+            break;
+        default:
+            hipLaunchKernelGGL((lut_matmul_kernel<T, 4>), grid, dim3(kThreads), lds, stream, blocks, xt, yt,
+                               partial, static_cast<int>(M), static_cast<int>(rows), G,
+                               plan.chunk_groups, plan.sub_groups);
+            break;
+    }
+    TQ1_LAUNCH_CHECK();
+    if (partial) {
+        const int64_t count = M * rows;
+        hipLaunchKernelGGL((reduce_partials_kernel<T>), dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, stream, partial, yt, count, plan.k_split);
+        TQ1_LAUNCH_CHECK();
+    }
+    return TERNEL_TQ1_OK;
+}
+
+struct GemmPlan {
+    int k_split;
+    int chunk_groups;
+    int64_t n_tiles;
+    int64_t m_tiles;
+};
+
+int plan_gemm(int64_t M, int64_t rows, int64_t columns, int k_split, GemmPlan *plan) {
+    const int64_t G = columns / kBlockWeights;
+    plan->n_tiles = (rows + kGemmBN - 1) / kGemmBN;
+    plan->m_tiles = (M + kGemmBM - 1) / kGemmBM;
+    if (plan->m_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");
+    if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
+    if (k_split == 0) {
+        const int64_t wgs = plan->n_tiles * plan->m_tiles;
+        k_split = wgs >= 512 ? 1 : largest_split(G, wgs * 2 > 0 ? wgs * 2 : 1);
+        // largest_split targets kSplitTargetWorkgroups; halve the ambition for
+        // the MFMA kernel, whose workgroups are heavier.
+    }
+    if (G % k_split)
+        return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row",
+                    k_split, static_cast<long long>(G));
+    plan->k_split = k_split;
+    plan->chunk_groups = static_cast<int>(G / k_split);
+    return TERNEL_TQ1_OK;
+}
+
+int launch_gemm(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows,
+                int64_t columns, const GemmPlan &plan, float *partial, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(plan.n_tiles), static_cast<unsigned>(plan.m_tiles),
+                    static_cast<unsigned>(plan.k_split));
+    hipLaunchKernelGGL(mfma_gemm_kernel, grid, dim3(kThreads), 0, stream, blocks,
+                       static_cast<const _Float16 *>(x), static_cast<_Float16 *>(y), partial,
+                       static_cast<int>(M), static_cast<int>(rows),
+                       static_cast<int>(columns / kBlockWeights), plan.chunk_groups);
+    TQ1_LAUNCH_CHECK();
+    if (partial) {
+        const int64_t count = M * rows;
+        hipLaunchKernelGGL((reduce_partials_kernel<_Float16>),
+                           dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                           stream, partial, static_cast<_Float16 *>(y), count, plan.k_split);
+        TQ1_LAUNCH_CHECK();
+    }
+    return TERNEL_TQ1_OK;
+}
+
+// The dispatch rule of packed_matmul, retuned for MI355X: the LUT23 kernel up
+// to this many activation rows, the MFMA kernel above it (fp16 only).
+constexpr int64_t kLinearLutMaxBatch = 4;
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char *ternel_tq1_last_error(void) { return g_last_error; }
+
+const char *ternel_tq1_version(void) { return "ternel-tq1-gfx950 0.1.0"; }
+
+int ternel_tq1_validate(const uint8_t *blocks, int64_t nblocks, uint64_t *counters, void *stream) {
+    g_last_error[0] = '\0';
+    if (!blocks || !counters) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (nblocks < 0) return fail(TERNEL_TQ1_EINVAL, "negative block count");
+    if (reinterpret_cast<uintptr_t>(blocks) & 3u)
+        return fail(TERNEL_TQ1_EINVAL, "blocks must be 4-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto *cnt = reinterpret_cast<unsigned long long *>(counters);
+    hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(64), 0, s, cnt, 2);
+    TQ1_LAUNCH_CHECK();
+    if (nblocks == 0) return TERNEL_TQ1_OK;
+    const int64_t nwords = nblocks * kBlockWords;
+    int64_t grid = (nwords + kThreads * 4 - 1) / (kThreads * 4);
+    if (grid > 8192) grid = 8192;
+    hipLaunchKernelGGL(validate_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
+                       reinterpret_cast<const uint32_t *>(blocks), nwords, cnt);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+int ternel_tq1_decode(const uint8_t *blocks, int64_t nblocks, uint8_t *scales_out, uint8_t *codes_out,
+                      void *stream) {
+    g_last_error[0] = '\0';
+    if (!blocks || !scales_out || !codes_out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (nblocks < 0) return fail(TERNEL_TQ1_EINVAL, "negative block count");
+    if (nblocks == 0) return TERNEL_TQ1_OK;
+    const int64_t threads = nblocks * kCodeSlots;
+    const int64_t grid = (threads + kThreads - 1) / kThreads;
+    if (grid > INT32_MAX) return fail(TERNEL_TQ1_EINVAL, "too many blocks for one decode launch");
+    hipLaunchKernelGGL(decode_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), blocks, nblocks, scales_out, codes_out);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int batch_tile,
+                                         int k_split) {
+    if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
+    LutPlan plan;
+    if (plan_lut(M, rows, columns, batch_tile, k_split, &plan) != TERNEL_TQ1_OK) return 0;
+    return plan.k_split > 1 ? static_cast<size_t>(plan.k_split) * M * rows * sizeof(float) : 0;
+}
+
+int ternel_tq1_matmul(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows,
+                      int64_t columns, int dtype, int batch_tile, int k_split, void *ws, size_t ws_bytes,
+                      void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
+    if (!blocks || !x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (reinterpret_cast<uintptr_t>(blocks) & 3u)
+        return fail(TERNEL_TQ1_EINVAL, "blocks must be 4-byte aligned");
+    LutPlan plan;
+    if ((rc = plan_lut(M, rows, columns, batch_tile, k_split, &plan)) != TERNEL_TQ1_OK) return rc;
+    if (plan.batch_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");
+    float *partial = nullptr;
+    if (plan.k_split > 1) {
+        const size_t need = static_cast<size_t>(plan.k_split) * M * rows * sizeof(float);
+        if (!ws || ws_bytes < need)
+            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs",
+                        ws_bytes, need);
+        partial = static_cast<float *>(ws);
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case TERNEL_TQ1_F16:
+            return launch_lut<_Float16>(blocks, x, y, M, rows, columns, plan, partial, s);
+        case TERNEL_TQ1_BF16:
+            return launch_lut<bf16_t>(blocks, x, y, M, rows, columns, plan, partial, s);
+        default:
+            return launch_lut<float>(blocks, x, y, M, rows, columns, plan, partial, s);
+    }
+}
+
+size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int k_split) {
+    if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
+    GemmPlan plan;
+    if (plan_gemm(M, rows, columns, k_split, &plan) != TERNEL_TQ1_OK) return 0;
+    return plan.k_split > 1 ? static_cast<size_t>(plan.k_split) * M * rows * sizeof(float) : 0;
+}
+
+int ternel_tq1_gemm(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+                    int dtype, int k_split, void *ws, size_t ws_bytes, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if (dtype != TERNEL_TQ1_F16)
+        return fail(TERNEL_TQ1_EINVAL, "the MFMA path takes fp16 activations, got dtype code %d", dtype);
+    if (!blocks || !x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(blocks) & 3u) || (reinterpret_cast<uintptr_t>(x) & 15u))
+        return fail(TERNEL_TQ1_EINVAL, "blocks must be 4-byte and activations 16-byte aligned");
+    GemmPlan plan;
+    if ((rc = plan_gemm(M, rows, columns, k_split, &plan)) != TERNEL_TQ1_OK) return rc;
+    float *partial = nullptr;
+    if (plan.k_split > 1) {
+        const size_t need = static_cast<size_t>(plan.k_split) * M * rows * sizeof(float);
+        if (!ws || ws_bytes < need)
+            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs",
+                        ws_bytes, need);
+        partial = static_cast<float *>(ws);
+    }
+    return launch_gemm(blocks, x, y, M, rows, columns, plan, partial, static_cast<hipStream_t>(stream));
+}
+
+int ternel_tq1_get_rows(const uint8_t *blocks, int64_t rows, int64_t columns, const int64_t *ids,
+                        int64_t n_ids, void *out, int dtype, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(1, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
+    if (n_ids <= 0) return fail(TERNEL_TQ1_EINVAL, "indices are empty");
+    if (!blocks || !ids || !out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    const int G = static_cast<int>(columns / kBlockWeights);
+    const int per_token = G * kCodeSlots;
+    const dim3 grid(static_cast<unsigned>((per_token + kThreads - 1) / kThreads),
+                    static_cast<unsigned>(n_ids < 65535 ? n_ids : 65535));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case TERNEL_TQ1_F16:
+            hipLaunchKernelGGL((get_rows_kernel<_Float16>), grid, dim3(kThreads), 0, s, blocks, rows, G, ids,
+                               n_ids, static_cast<_Float16 *>(out));
+            break;
+        case TERNEL_TQ1_BF16:
+            hipLaunchKernelGGL((get_rows_kernel<bf16_t>), grid, dim3(kThreads), 0, s, blocks, rows, G, ids,
+                               n_ids, static_cast<bf16_t *>(out));
+            break;
+        default:
+            hipLaunchKernelGGL((get_rows_kernel<float>), grid, dim3(kThreads), 0, s, blocks, rows, G, ids,
+                               n_ids, static_cast<float *>(out));
+            break;
+    }
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
+    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
+        return ternel_tq1_matmul_workspace_bytes(M, rows, columns, 0, 0);
+    return ternel_tq1_gemm_workspace_bytes(M, rows, columns, 0);
+}
+
+int ternel_tq1_linear(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+                      int dtype, void *ws, size_t ws_bytes, void *stream) {
+    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
+        return ternel_tq1_matmul(blocks, x, y, M, rows, columns, dtype, 0, 0, ws, ws_bytes, stream);
+    return ternel_tq1_gemm(blocks, x, y, M, rows, columns, dtype, 0, ws, ws_bytes, stream);
+}
+
+}  // extern "C"

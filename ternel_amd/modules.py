@@ -1,0 +1,179 @@
+"""torch modules that execute packed TQ1_G128 weights without unpacking them.
+
+Twins of the reference's module API (src/ternel_mlx/modules.py:425-549):
+``packed_matmul``, ``PackedLinear`` and ``PackedEmbedding`` keep their names,
+constructor arguments, call signatures, output shapes/dtypes and FormatError
+messages. The only parameter a module owns is its packed weight -- here the
+canonical ``blocks`` buffer ``(rows, groups_per_row, 28)`` uint8, the exact
+bytes the gfx950 kernels stream -- and the reference's tiled ``codes``/``scales``
+pair is accepted on load (``load_packed``) and exposed as properties, both by
+exact byte permutation.
+
+``replace_with_packed`` is the torch counterpart of
+src/ternel_mlx/packed_model.py:72-92: it swaps every bias-free ``nn.Linear`` and
+every ``nn.Embedding`` of a model for the packed twins.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+from torch import nn
+
+from .format import BLOCK_BYTES, FormatError, as_device_blocks, validate_packed_codes
+from .kernels import GemmConfig, MatmulConfig, tq1_gemm, tq1_get_rows, tq1_matmul
+from .layout import PackedTensorLayout, pack_blocks, unpack_blocks
+
+# Dispatch (src/ternel_mlx/modules.py:331-422, re-measured for MI355X): the
+# LUT23 kernel for batches up to LUT23_MAX_BATCH, the MFMA kernel above it.
+# The LUT kernel's cost grows linearly with the batch (one table set per
+# vector) while its bytes do not, so it only pays while the weight stream
+# dominates; the MFMA kernel decodes each weight once per 128-row batch tile.
+LUT23_MAX_BATCH = 4
+
+
+def select_kernel(layout: PackedTensorLayout, batch: int, dtype: torch.dtype) -> str:
+    """``"lut23"`` or ``"gemm"`` for ``batch`` activation rows."""
+    if batch <= LUT23_MAX_BATCH or dtype != torch.float16:
+        return "lut23"
+    return "gemm"
+
+
+def packed_matmul(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+    """``x @ W.T`` for a packed ``W``, choosing the kernel by activation rows.
+
+    Leading dimensions of ``x`` are kept (src/ternel_mlx/modules.py:425-457).
+    """
+    if x.shape[-1] != layout.columns:
+        raise FormatError(f"activation has {x.shape[-1]} columns, weight expects {layout.columns}")
+    flat = x.reshape(-1, layout.columns)
+    if select_kernel(layout, flat.shape[0], flat.dtype) == "gemm":
+        out = tq1_gemm(blocks, flat, layout=layout, config=GemmConfig())
+    else:
+        out = tq1_matmul(blocks, flat, layout=layout, config=MatmulConfig())
+    return out.reshape(*x.shape[:-1], layout.rows)
+
+
+class _PackedWeight(nn.Module):
+    """Shared storage and loading of one packed weight."""
+
+    def __init__(self, layout: PackedTensorLayout, device=None) -> None:
+        super().__init__()
+        self.layout = layout
+        if device is None and torch.cuda.is_available():
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.register_buffer("blocks", torch.zeros(layout.canonical_shape, dtype=torch.uint8, device=device))
+
+    def load_blocks(self, blocks, *, validate: bool = True) -> None:
+        """Load canonical blocks (any shape holding ``rows * G`` 28-byte blocks)."""
+        tensor = as_device_blocks(blocks)
+        if tensor.shape[0] != self.layout.groups:
+            raise FormatError(
+                f"expected {self.layout.groups} blocks for {self.layout.rows}x{self.layout.columns}, "
+                f"got {tensor.shape[0]}"
+            )
+        if validate:
+            validate_packed_codes(tensor)
+        self.blocks = tensor.reshape(self.layout.canonical_shape).to(self.blocks.device)
+
+    def load_packed(self, codes, scales, *, validate: bool = True) -> None:
+        """Load the reference's tiled ``codes`` (u8) / ``scales`` (<u2) arrays."""
+        codes_np = codes.cpu().numpy() if isinstance(codes, torch.Tensor) else np.asarray(codes)
+        scales_np = scales.cpu().numpy() if isinstance(scales, torch.Tensor) else np.asarray(scales)
+        if scales_np.dtype == np.int16:
+            scales_np = scales_np.view("<u2")
+        self.load_blocks(unpack_blocks(codes_np, scales_np, layout=self.layout), validate=validate)
+
+    def load_weights(self, weights, strict: bool = True) -> "_PackedWeight":
+        """MLX-style ``load_weights([("codes", c), ("scales", s)])`` (tests/test_mlx_modules.py:132-133)."""
+        named = dict(weights)
+        if "blocks" in named:
+            self.load_blocks(named.pop("blocks"))
+        elif "codes" in named or "scales" in named:
+            if "codes" not in named or "scales" not in named:
+                raise FormatError("codes and scales must be loaded together")
+            self.load_packed(named.pop("codes"), named.pop("scales"))
+        if strict and named:
+            raise FormatError(f"unexpected weights: {sorted(named)}")
+        return self
+
+    @property
+    def codes(self) -> np.ndarray:
+        """The reference's tiled code array, by exact permutation of ``blocks``."""
+        return pack_blocks(self.blocks.cpu().numpy(), layout=self.layout)[0]
+
+    @property
+    def scales(self) -> np.ndarray:
+        """The reference's tiled scale array (raw fp16 bits as <u2)."""
+        return pack_blocks(self.blocks.cpu().numpy(), layout=self.layout)[1]
+
+
+class PackedLinear(_PackedWeight):
+    """Bias-free linear layer whose weight stays in TQ1_G128 (src/ternel_mlx/modules.py:460-495)."""
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear) -> "PackedLinear":
+        if linear.bias is not None:
+            raise FormatError("a packed linear layer cannot carry a bias")
+        rows, columns = linear.weight.shape
+        return cls(PackedTensorLayout.for_tensor(rows, columns), device=linear.weight.device)
+
+    def extra_repr(self) -> str:
+        return (f"{self.layout.columns} -> {self.layout.rows}, tile={self.layout.tile}, "
+                f"{self.layout.bits_per_weight:.3f} bits/weight")
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return packed_matmul(self.blocks, x, layout=self.layout)
+
+
+class PackedEmbedding(_PackedWeight):
+    """Token embedding decoded one row at a time (src/ternel_mlx/modules.py:498-549)."""
+
+    def __init__(self, layout: PackedTensorLayout, *, dtype: torch.dtype, device=None) -> None:
+        super().__init__(layout, device=device)
+        self.dtype = dtype
+
+    @classmethod
+    def from_embedding(cls, embedding: nn.Embedding, *, dtype: torch.dtype) -> "PackedEmbedding":
+        rows, columns = embedding.weight.shape
+        return cls(PackedTensorLayout.for_tensor(rows, columns), dtype=dtype, device=embedding.weight.device)
+
+    def extra_repr(self) -> str:
+        return f"{self.layout.rows} x {self.layout.columns}, tile={self.layout.tile}, {self.dtype}"
+
+    def forward(self, indices: torch.Tensor) -> torch.Tensor:
+        """Rows for ``indices`` of any shape; ids outside the table read as zeros."""
+        flat = indices.reshape(-1)
+        rows = tq1_get_rows(self.blocks, flat, layout=self.layout, dtype=self.dtype)
+        return rows.reshape(*indices.shape, self.layout.columns)
+
+    def as_linear(self, x: torch.Tensor) -> torch.Tensor:
+        """Tied output head: the embedding table used as a matmul."""
+        return packed_matmul(self.blocks, x, layout=self.layout)
+
+
+def replace_with_packed(model: nn.Module, *, embedding_dtype: torch.dtype = torch.float16) -> nn.Module:
+    """Swap every bias-free ``nn.Linear`` and every ``nn.Embedding`` for its packed twin.
+
+    The packed modules start zero-filled; their weights arrive through
+    ``load_blocks``/``load_packed``/``load_weights``.
+    """
+    for name, child in list(model.named_children()):
+        if isinstance(child, nn.Linear) and child.bias is None and child.in_features % 128 == 0:
+            setattr(model, name, PackedLinear.from_linear(child))
+        elif isinstance(child, nn.Embedding) and child.embedding_dim % 128 == 0:
+            setattr(model, name, PackedEmbedding.from_embedding(child, dtype=embedding_dtype))
+        else:
+            replace_with_packed(child, embedding_dtype=embedding_dtype)
+    return model
+
+
+__all__ = [
+    "BLOCK_BYTES",
+    "LUT23_MAX_BATCH",
+    "PackedEmbedding",
+    "PackedLinear",
+    "packed_matmul",
+    "replace_with_packed",
+    "select_kernel",
+]

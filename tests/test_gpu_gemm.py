@@ -1,0 +1,125 @@
+"""MFMA prefill kernel against the fp64 oracle.
+
+Weights decode to fp16 (t - 1) * scale exactly and fp16 x fp16 products are
+exact in fp32, so the only roundings are the fp32 accumulation and the final
+fp16 store. Each element is therefore held to one fp16 rounding of the oracle
+plus an fp32 accumulation bound, and every case to the north star's 1e-3
+case-normalised error.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq1_oracle as O
+from tests.gpu_util import layout, random_blocks, to_dev
+from ternel_amd.format import FormatError
+from ternel_amd.kernels import GemmConfig, tq1_gemm
+
+pytestmark = pytest.mark.gpu
+
+NORTH_STAR_TOLERANCE = 1e-3
+FP16_UNIT_ROUNDOFF = 2.0 ** -11
+
+
+def run(blocks: np.ndarray, x16: np.ndarray, *, k_split: int = 0) -> np.ndarray:
+    rows, g, _ = blocks.shape
+    out = tq1_gemm(to_dev(blocks), to_dev(x16), layout=layout(rows, g * 128), config=GemmConfig(k_split=k_split))
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy().astype(np.float64)
+
+
+def assert_fp16_faithful(got: np.ndarray, blocks: np.ndarray, x16: np.ndarray) -> None:
+    rows, g, _ = blocks.shape
+    columns = g * 128
+    x = x16.astype(np.float64)
+    oracle = O.oracle_matmul(blocks, x, rows=rows, columns=columns)
+    weights = O.dense_weights(blocks, rows=rows, columns=columns)
+    terms = np.abs(x) @ np.abs(weights).T
+    accumulation = columns * float(np.finfo(np.float32).eps) * terms
+    # fp16 store: half an ulp of the (accumulated) value, incl. subnormal spacing.
+    store = FP16_UNIT_ROUNDOFF * (np.abs(oracle) + accumulation) + 2.0 ** -25
+    assert (np.abs(got - oracle) <= accumulation + store).all()
+    result = O.compare(got, oracle)
+    assert result["normalised_max_abs_error"] < NORTH_STAR_TOLERANCE
+    assert result["pattern_mismatches"] == 0
+
+
+def test_mfma_lane_layout_probe() -> None:
+    """Identity activations pick out single weights: y[m][n] = W[n][m] for m < 128.
+
+    A transposed operand or a wrong accumulator lane map moves values to other
+    positions, which this catches element by element.
+    """
+    rows, columns = 256, 128
+    blocks = random_blocks(rows, columns, seed=11)
+    x = np.eye(128, columns, dtype=np.float16)
+    got = run(blocks, x)
+    weights = O.dense_weights(blocks, rows=rows, columns=columns).astype(np.float16).astype(np.float64)
+    np.testing.assert_array_equal(got, weights.T[:128])
+
+
+SHAPES = ((48, 5120), (256, 640), (512, 384), (1024, 5120), (300, 256))
+
+
+@pytest.mark.parametrize(("rows", "columns"), SHAPES)
+@pytest.mark.parametrize("batch", (1, 5, 33, 64, 130, 256))
+def test_gemm_matches_the_oracle(rows: int, columns: int, batch: int) -> None:
+    blocks = random_blocks(rows, columns, seed=rows * 31 + columns)
+    x = np.random.default_rng(rows + columns + batch).normal(0.0, 1.0, size=(batch, columns)).astype(np.float16)
+    assert_fp16_faithful(run(blocks, x), blocks, x)
+
+
+@pytest.mark.parametrize("k_split", (1, 2, 5, 8, 40))
+def test_gemm_split_k_matches_the_oracle(k_split: int) -> None:
+    blocks = random_blocks(384, 5120, seed=k_split)
+    x = np.random.default_rng(k_split).normal(0.0, 0.5, size=(37, 5120)).astype(np.float16)
+    assert_fp16_faithful(run(blocks, x, k_split=k_split), blocks, x)
+
+
+def test_gemm_split_k_is_exact_on_integer_data() -> None:
+    rows, groups = 256, 40
+    rng = np.random.default_rng(3)
+    scales = np.full(rows * groups, 1.0, dtype=np.float16).view(np.uint8).reshape(-1, 2)
+    trits = rng.integers(0, 3, size=(rows * groups, 128), dtype=np.uint8)
+    blocks = O.encode_tq1_blocks(scales, trits).reshape(rows, groups, 28)
+    x = rng.choice((-1.0, 1.0), size=(20, groups * 128)).astype(np.float16)
+    want = O.oracle_matmul(blocks, x.astype(np.float64), rows=rows, columns=groups * 128)
+    # Integer results up to 5120 in magnitude are exact in fp16 only below 2048;
+    # compare through fp16 rounding of the exact answer.
+    want16 = want.astype(np.float16).astype(np.float64)
+    for k in (1, 2, 4, 5, 8, 10, 20, 40):
+        np.testing.assert_array_equal(run(blocks, x, k_split=k), want16, err_msg=f"k_split={k}")
+
+
+def test_gemm_is_deterministic() -> None:
+    blocks = random_blocks(512, 5120, seed=5)
+    x = np.random.default_rng(5).normal(0, 1, size=(64, 5120)).astype(np.float16)
+    first = run(blocks, x, k_split=8)
+    for _ in range(2):
+        np.testing.assert_array_equal(run(blocks, x, k_split=8), first)
+
+
+def test_gemm_propagates_non_finite_activations() -> None:
+    blocks = random_blocks(256, 384, seed=7)
+    x = np.zeros((3, 384), dtype=np.float16)
+    x[0, 0] = np.nan
+    x[1, 125] = np.inf
+    x[2, 383] = -np.inf
+    got = run(blocks, x)
+    want = O.oracle_matmul(blocks, x.astype(np.float64), rows=256, columns=384)
+    assert O.compare(got, want)["pattern_mismatches"] == 0
+
+
+def test_gemm_rejects_other_dtypes_and_bad_splits() -> None:
+    blocks = to_dev(random_blocks(256, 384, seed=1))
+    lay = layout(256, 384)
+    with pytest.raises(FormatError, match="float16"):
+        tq1_gemm(blocks, torch.zeros((4, 384), device="cuda"), layout=lay)
+    with pytest.raises(FormatError, match="does not divide the tensor's 3 groups"):
+        tq1_gemm(blocks, torch.zeros((4, 384), device="cuda", dtype=torch.float16), layout=lay,
+                 config=GemmConfig(k_split=2))
+    with pytest.raises(FormatError, match="activations have 256 columns, expected 384"):
+        tq1_gemm(blocks, torch.zeros((4, 256), device="cuda", dtype=torch.float16), layout=lay)
