@@ -120,7 +120,7 @@ def main() -> int:
     import torch
 
     from ternel_amd import synthetic
-    from ternel_amd.kernels import GemmConfig, MatmulConfig, tq1_gemm, tq1_matmul
+    from ternel_amd.kernels import GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_matmul
     from ternel_amd.layout import PackedTensorLayout
 
     dev = torch.device("cuda", 0)
@@ -131,8 +131,8 @@ def main() -> int:
     step_bytes = sum(packed_bytes(K, N) for _, K, N in C1_SHAPES)
     ring = max(2, -(-RING_BYTES_MIN // step_bytes))
     layouts = [PackedTensorLayout.for_tensor(N, K) for _, K, N in C1_SHAPES]
-    weights = [[synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i)
-                for i, (_, K, N) in enumerate(C1_SHAPES)] for r in range(ring)]
+    weights = [[pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
+                for i, ((_, K, N), lay) in enumerate(zip(C1_SHAPES, layouts))] for r in range(ring)]
     xs = [synthetic.device_activations(1, K, seed=synthetic.SEED_BASE + 1 + i) for i, (_, K, _) in enumerate(C1_SHAPES)]
     config = MatmulConfig()
 
@@ -212,7 +212,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "gate/up GEMV 5120->17408 (lut_matmul_kernel<_Float16,1> + ordered split-K reduction)",
+            "kernel": "gate/up GEMV 5120->17408 (lut_gemv_kernel, fused ordered split-K)",
             "bytes_per_launch": dom_bytes,
         },
     }
@@ -222,7 +222,7 @@ def main() -> int:
         prefill = {}
         for name, K, N in C3_SHAPES:
             lay = PackedTensorLayout.for_tensor(N, K)
-            blk = synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3)
+            blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
             xp = synthetic.device_activations(512, K, seed=synthetic.SEED_BASE + 3, sigma=0.5)
             for _ in range(3):
                 tq1_gemm(blk, xp, layout=lay, config=GemmConfig())

@@ -28,8 +28,11 @@ _size = ctypes.c_size_t
 SIGNATURES = {
     "ternel_tq1_last_error": (ctypes.c_char_p, []),
     "ternel_tq1_version": (ctypes.c_char_p, []),
+    "ternel_tq1_packed_words": (_i64, [_i64, _i64]),
     "ternel_tq1_validate": (_int, [_p, _i64, _p, _p]),
     "ternel_tq1_decode": (_int, [_p, _i64, _p, _p, _p]),
+    "ternel_tq1_interleave": (_int, [_p, _i64, _i64, _p, _p]),
+    "ternel_tq1_deinterleave": (_int, [_p, _i64, _i64, _p, _p]),
     "ternel_tq1_matmul": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p, _size, _p]),
     "ternel_tq1_matmul_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
     "ternel_tq1_gemm": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _p, _size, _p]),

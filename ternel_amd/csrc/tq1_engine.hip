@@ -1,14 +1,25 @@
 // tq1_engine.hip -- TQ1_G128 packed-weight kernels for MI355X (gfx950, CDNA4).
 //
-// One shared library, C ABI only (include/ternel_tq1.h). All kernels read the
-// canonical 28-byte blocks straight from HBM; nothing model-sized is ever
-// expanded. Kernels:
-//   validate_kernel   fail-closed byte scan (regular > 242, tail > 26)
-//   decode_kernel     bit-exact trit decode (test / inspection entry)
-//   lut_matmul_kernel LUT23 product for M = 1 (decode GEMV) and small batches
-//   mfma_gemm_kernel  trits -> fp16 LDS tiles -> v_mfma_f32_32x32x16_f16
-//   get_rows_kernel   packed embedding-row gather
-// plus an ordered split-K reduction and small helpers.
+// One shared library, C ABI only (include/ternel_tq1.h).
+//
+// Device layout ("packed"): the canonical 28-byte blocks, permuted at 4-byte
+// granularity into 64-row tiles -- word j (bytes 4j..4j+3) of block (row r,
+// group g) lives at packed[((r / 64) * G + g) * 7 + j][r % 64]. A wave64 whose
+// lanes own 64 consecutive rows therefore reads one word of one group with a
+// single fully coalesced 256-byte load, and a tile of rows for one group is one
+// contiguous 1,792-byte run. Rows past the end of the last tile are zero words.
+// The permutation is exact in both directions (interleave_kernel /
+// deinterleave_kernel); nothing is re-encoded, the weight stays 28 bytes per
+// 128 weights.
+//
+// Kernels:
+//   validate_kernel    fail-closed byte scan of canonical blocks
+//   decode_kernel      bit-exact trit decode of canonical blocks (test entry)
+//   interleave_kernel / deinterleave_kernel   canonical <-> packed
+//   lut_gemv_kernel    LUT23 product, M = 1 decode GEMV and small batches,
+//                      with a fused, ordered split-K fix-up
+//   mfma_gemm_kernel   trits -> fp16 LDS tiles -> v_mfma_f32_32x32x16_f16
+//   get_rows_kernel    packed embedding-row gather
 
 #include <hip/hip_runtime.h>
 
@@ -19,17 +30,19 @@
 
 #include "ternel_tq1.h"
 
-// ---------------------------------------------------------------------------
-// Format constants (src/bonsai_tq1/format.py:14-24, lut23_reorder.py:27-29)
-// ---------------------------------------------------------------------------
 namespace {
 
+// Format constants (src/bonsai_tq1/format.py:14-24, lut23_reorder.py:27-29).
 constexpr int kBlockWeights = 128;
 constexpr int kBlockBytes = 28;
 constexpr int kBlockWords = 7;
 constexpr int kCodeSlots = 26;
 constexpr int kFullSlots = 25;
 constexpr uint32_t kMaxTailByte = 26;
+
+// Packed layout: 64-row tiles, 7 words per block.
+constexpr int kTileRows = 64;
+constexpr int kTileGroupWords = kBlockWords * kTileRows;  // 448 words per (tile, group)
 
 // LUT23 tables of one 128-weight group, fp32: L2[25][9] over trits (0,1) of a
 // slot, L3[25][27] over trits (2,3,4), tail[27] over trits 125..127.
@@ -38,6 +51,7 @@ constexpr int kL3Entries = 27;
 constexpr int kL3Base = kFullSlots * kL2Entries;             // 225
 constexpr int kTailBase = kL3Base + kFullSlots * kL3Entries;  // 900
 constexpr int kLutFloats = kTailBase + 27;                    // 927
+constexpr int kTasksPerGroup = 2 * kFullSlots + 1;            // L2 x25, L3 x25, tail
 
 constexpr int kThreads = 256;
 
@@ -50,13 +64,6 @@ int fail(int code, const char *fmt, ...) {
     va_end(ap);
     return code;
 }
-
-#define TQ1_HIP_CHECK(expr)                                                                   \
-    do {                                                                                      \
-        hipError_t err_ = (expr);                                                             \
-        if (err_ != hipSuccess)                                                               \
-            return fail(TERNEL_TQ1_EHIP, "%s failed: %s", #expr, hipGetErrorString(err_));    \
-    } while (0)
 
 #define TQ1_LAUNCH_CHECK()                                                                    \
     do {                                                                                      \
@@ -128,6 +135,10 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
     return v;
 }
 
+__device__ __forceinline__ int64_t packed_word_index(int64_t row, int64_t G, int64_t g, int j) {
+    return (((row / kTileRows) * G + g) * kBlockWords + j) * kTileRows + (row % kTileRows);
+}
+
 // ---------------------------------------------------------------------------
 // Helpers
 // ---------------------------------------------------------------------------
@@ -137,8 +148,8 @@ __global__ void zero_u64_kernel(unsigned long long *p, int n) {
 }
 
 // ---------------------------------------------------------------------------
-// validate_kernel: counts regular code bytes > 242 and tail bytes > 26.
-// The buffer is walked as 32-bit words; word j (0..6) of a block holds
+// validate_kernel: counts regular code bytes > 242 and tail bytes > 26 in
+// canonical blocks, walked as 32-bit words; word j (0..6) of a block holds
 //   j = 0: scale, scale, code0, code1      j = 1..5: four codes
 //   j = 6: code22, code23, code24, tail.
 // SWAR per byte b:  b >= 243  <=>  bit7(b) & bit7((b & 0x7f) + 13)
@@ -202,13 +213,43 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const uint8_t *__restr
 }
 
 // ---------------------------------------------------------------------------
+// interleave_kernel / deinterleave_kernel: canonical blocks <-> packed words.
+// One thread per packed word (writes coalesced) / per canonical word.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void interleave_kernel(const uint32_t *__restrict__ canonical,
+                                                              uint32_t *__restrict__ packed, int64_t rows,
+                                                              int64_t G, int64_t total_words) {
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (w >= total_words) return;
+    const int lane = static_cast<int>(w % kTileRows);
+    const int64_t rest = w / kTileRows;
+    const int j = static_cast<int>(rest % kBlockWords);
+    const int64_t tg = rest / kBlockWords;
+    const int64_t g = tg % G;
+    const int64_t row = (tg / G) * kTileRows + lane;
+    packed[w] = row < rows ? canonical[(row * G + g) * kBlockWords + j] : 0u;
+}
+
+__global__ __launch_bounds__(kThreads) void deinterleave_kernel(const uint32_t *__restrict__ packed,
+                                                                uint32_t *__restrict__ canonical, int64_t G,
+                                                                int64_t total_words) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (c >= total_words) return;
+    const int j = static_cast<int>(c % kBlockWords);
+    const int64_t rg = c / kBlockWords;
+    const int64_t g = rg % G;
+    const int64_t row = rg / G;
+    canonical[c] = packed[packed_word_index(row, G, g, j)];
+}
+
+// ---------------------------------------------------------------------------
 // get_rows_kernel: one thread per (token, group, code slot) writes the 5 (or
 // 3) weights that byte holds: (t - 1) * scale, evaluated in fp32 and rounded
 // to T (exact for fp16 and fp32). Ids outside [0, rows) give zeros
 // (src/ternel_mlx/kernels.py:869-880).
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint8_t *__restrict__ blocks,
+__global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__restrict__ packed,
                                                             int64_t rows, int G,
                                                             const int64_t *__restrict__ ids,
                                                             int64_t n_ids, T *__restrict__ out) {
@@ -219,6 +260,7 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint8_t *__res
     const int s = i - g * kCodeSlots;
     const int first = s < kFullSlots ? 5 * s : 125;
     const int count = s < kFullSlots ? 5 : 3;
+    const int byte_index = 2 + s;
     for (int64_t t = blockIdx.y; t < n_ids; t += gridDim.y) {
         const int64_t id = ids[t];
         T *o = out + t * static_cast<int64_t>(G) * kBlockWeights + g * kBlockWeights + first;
@@ -226,10 +268,8 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint8_t *__res
             for (int d = 0; d < count; ++d) o[d] = from_f32<T>(0.0f);
             continue;
         }
-        const uint8_t *blk = blocks + (id * G + g) * kBlockBytes;
-        const float scale = half_bits_to_float(static_cast<uint32_t>(blk[0]) |
-                                               (static_cast<uint32_t>(blk[1]) << 8));
-        uint32_t b = blk[2 + s];
+        const float scale = half_bits_to_float(packed[packed_word_index(id, G, g, 0)]);
+        uint32_t b = (packed[packed_word_index(id, G, g, byte_index >> 2)] >> ((byte_index & 3) * 8)) & 0xffu;
         for (int d = 0; d < count; ++d) {
             const uint32_t q = b / 3u;
             const uint32_t trit = b - 3u * q;
@@ -240,134 +280,164 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint8_t *__res
 }
 
 // ---------------------------------------------------------------------------
-// lut_matmul_kernel: LUT23 product (the algorithm of src/ternel_mlx/kernels.py
-// :244-342, re-designed for wave64 and canonical blocks).
+// lut_gemv_kernel: the LUT23 product (algorithm of src/ternel_mlx/kernels.py
+// :244-342), re-designed for wave64 on the packed layout.
 //
-// Grid (row tiles of 256, batch tiles of BT, K chunks). A workgroup builds the
-// LUT23 tables of up to `sub_groups` groups x BT activation vectors in LDS,
-// then each lane streams its own row's 28-byte blocks for those groups (seven
-// dword loads, one block of prefetch) and, per code byte p, adds
-// L2[s][p % 9] + L3[s][p / 9] (hi = (p * 57) >> 9, lo = p - 9 hi). All lanes of
-// a wave index the same slot's 9- or 27-entry table, which sit in distinct LDS
-// banks, so the lookups are conflict-free. Per group: acc = fma(scale, sum, acc)
-// with the raw fp16 scale, the summation order of the reference kernel.
-// With more than one K chunk the fp32 partials go to `partial` and
-// reduce_partials_kernel adds them in chunk order (deterministic).
-// Illegal regular bytes stay inside the group's 927-entry table; the tail index
-// is clamped, so no input reads outside the tables.
+// Grid (row blocks of 256 = four 64-row tiles, batch tiles of BT, K chunks of
+// C groups). Each lane owns one row. The kernel
+//   1. issues all C x 7 word loads of its row up front (one coalesced 256-byte
+//      load per wave per word), so the whole weight stream is in flight while
+//   2. the workgroup builds the LUT23 tables of its C groups x BT vectors in
+//      LDS: 51 tasks per (vector, group) -- 25 L2 slots, 25 L3 slots, the
+//      tail -- each computing its 9 or 27 entries from 2-3 activations;
+//   3. per code byte p adds L2[s][p % 9] + L3[s][p / 9] (hi = (p*57) >> 9).
+//      All lanes of a wave index the same slot's 9- or 27-entry table, which
+//      sit in distinct LDS banks, so every lookup is conflict-free; the table
+//      base is a compile-time offset, so a lookup's address is just 4*lo or
+//      4*hi. Per group: acc = fma(scale, sum, acc) with the raw fp16 scale --
+//      the reference's summation order, so an unsplit launch is bit-exact
+//      with it;
+//   4. with one K chunk writes y; otherwise writes its fp32 partial, and the
+//      last workgroup of the row block to arrive (agent-scope counter) adds
+//      the chunks in chunk order -- deterministic -- writes y and re-arms the
+//      counter to zero.
+// Illegal regular bytes index inside the group's 927 entries and the tail is
+// clamped, so no input reads outside the tables.
 // ---------------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ float lut_entry(const T *__restrict__ xg, int idx) {
-    if (idx < kL3Base) {
-        const int s = idx / kL2Entries;
-        const int c = idx - s * kL2Entries;
-        const float x0 = to_f32<T>(xg[5 * s]);
-        const float x1 = to_f32<T>(xg[5 * s + 1]);
-        return (static_cast<float>(c % 3) - 1.0f) * x0 + (static_cast<float>(c / 3) - 1.0f) * x1;
+template <typename T, int C, int BT>
+__device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats], const T *__restrict__ x,
+                                                 int64_t K, int M, int b0, int g0, int tid) {
+    for (int task = tid; task < BT * C * kTasksPerGroup; task += kThreads) {
+        const int j = task / (C * kTasksPerGroup);
+        const int rem = task - j * (C * kTasksPerGroup);
+        const int c = rem / kTasksPerGroup;
+        const int k = rem - c * kTasksPerGroup;
+        const int sample = min(b0 + j, M - 1);
+        const T *xg = x + static_cast<int64_t>(sample) * K + static_cast<int64_t>(g0 + c) * kBlockWeights;
+        float *L = lut[j][c];
+        if (k < kFullSlots) {
+            const float x0 = to_f32<T>(xg[5 * k]);
+            const float x1 = to_f32<T>(xg[5 * k + 1]);
+            const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
+            const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
+            float *dst = L + k * kL2Entries;
+#pragma unroll
+            for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
+        } else {
+            const int s = k - kFullSlots;
+            const int base = s < kFullSlots ? 5 * s + 2 : 125;
+            const float x2 = to_f32<T>(xg[base]);
+            const float x3 = to_f32<T>(xg[base + 1]);
+            const float x4 = to_f32<T>(xg[base + 2]);
+            const float a[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
+            const float b[3] = {-1.0f * x3, 0.0f * x3, 1.0f * x3};
+            const float d[3] = {-1.0f * x4, 0.0f * x4, 1.0f * x4};
+            float *dst = L + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
+#pragma unroll
+            for (int e = 0; e < kL3Entries; ++e) dst[e] = (a[e % 3] + b[(e / 3) % 3]) + d[e / 9];
+        }
     }
-    if (idx < kTailBase) {
-        const int e = idx - kL3Base;
-        const int s = e / kL3Entries;
-        const int c = e - s * kL3Entries;
-        const float x2 = to_f32<T>(xg[5 * s + 2]);
-        const float x3 = to_f32<T>(xg[5 * s + 3]);
-        const float x4 = to_f32<T>(xg[5 * s + 4]);
-        return (static_cast<float>(c % 3) - 1.0f) * x2 +
-               (static_cast<float>((c / 3) % 3) - 1.0f) * x3 +
-               (static_cast<float>(c / 9) - 1.0f) * x4;
-    }
-    const int c = idx - kTailBase;
-    const float x0 = to_f32<T>(xg[125]);
-    const float x1 = to_f32<T>(xg[126]);
-    const float x2 = to_f32<T>(xg[127]);
-    return (static_cast<float>(c % 3) - 1.0f) * x0 +
-           (static_cast<float>((c / 3) % 3) - 1.0f) * x1 +
-           (static_cast<float>(c / 9) - 1.0f) * x2;
 }
 
-template <typename T, int BT>
-__global__ __launch_bounds__(kThreads) void lut_matmul_kernel(
-    const uint8_t *__restrict__ blocks, const T *__restrict__ x, T *__restrict__ y,
-    float *__restrict__ partial, int M, int N, int G, int chunk_groups, int sub_groups) {
-    extern __shared__ float lut[];
+template <typename T, int C, int BT>
+__global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
+    const uint32_t *__restrict__ packed, const T *__restrict__ x, T *__restrict__ y,
+    float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
+    int k_split) {
+    __shared__ float lut[BT][C][kLutFloats];
+    __shared__ unsigned s_last;
+
     const int tid = threadIdx.x;
-    const int row = blockIdx.x * kThreads + tid;
-    const int batch0 = blockIdx.y * BT;
-    const int chunk = blockIdx.z;
-    const int g_begin = chunk * chunk_groups;
-    const int g_end = min(G, g_begin + chunk_groups);
+    const int lane = tid & 63;
+    const int tile = blockIdx.x * (kThreads / kTileRows) + (tid >> 6);
+    const int row = tile * kTileRows + lane;
+    const bool row_ok = row < N;
+    const int b0 = blockIdx.y * BT;
+    const int g_begin = blockIdx.z * chunk_groups;
+    const int g_end = g_begin + chunk_groups;
     const int64_t K = static_cast<int64_t>(G) * kBlockWeights;
-    const uint32_t *row_words =
-        reinterpret_cast<const uint32_t *>(blocks) + static_cast<int64_t>(row) * G * kBlockWords;
+    const uint32_t *row_words = packed + static_cast<int64_t>(tile) * G * kTileGroupWords + lane;
 
     float acc[BT];
 #pragma unroll
     for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
 
-    for (int g0 = g_begin; g0 < g_end; g0 += sub_groups) {
-        const int ng = min(sub_groups, g_end - g0);
-        __syncthreads();  // previous tables fully consumed
-        const int per_vector = ng * kLutFloats;
-        for (int e = tid; e < BT * per_vector; e += kThreads) {
-            const int j = e / per_vector;
-            const int rem = e - j * per_vector;
-            const int gi = rem / kLutFloats;
-            const int idx = rem - gi * kLutFloats;
-            const int sample = min(batch0 + j, M - 1);
-            const T *xg = x + static_cast<int64_t>(sample) * K +
-                          static_cast<int64_t>(g0 + gi) * kBlockWeights;
-            lut[(j * sub_groups + gi) * kLutFloats + idx] = lut_entry<T>(xg, idx);
+    for (int g0 = g_begin; g0 < g_end; g0 += C) {
+        // 1. This row's C blocks, in flight before the tables are built.
+        uint32_t w[C][kBlockWords];
+        if (row_ok) {
+            const uint32_t *p = row_words + static_cast<int64_t>(g0) * kTileGroupWords;
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int j = 0; j < kBlockWords; ++j) w[c][j] = p[(c * kBlockWords + j) * kTileRows];
         }
+
+        // 2. Tables (after every lane is done reading the previous ones).
+        if (g0 != g_begin) __syncthreads();
+        build_lut_tables<T, C, BT>(lut, x, K, M, b0, g0, tid);
         __syncthreads();
-        if (row < N) {
-            uint32_t w[kBlockWords], nw[kBlockWords];
-            const uint32_t *bp = row_words + static_cast<int64_t>(g0) * kBlockWords;
+
+        // 3. Consume.
+        if (row_ok) {
 #pragma unroll
-            for (int k = 0; k < kBlockWords; ++k) w[k] = bp[k];
-            for (int gi = 0; gi < ng; ++gi) {
-                if (gi + 1 < ng) {
-#pragma unroll
-                    for (int k = 0; k < kBlockWords; ++k) nw[k] = bp[(gi + 1) * kBlockWords + k];
-                }
-                const float scale = half_bits_to_float(w[0]);
+            for (int c = 0; c < C; ++c) {
+                const float scale = half_bits_to_float(w[c][0]);
                 float sum[BT];
 #pragma unroll
                 for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
 #pragma unroll
                 for (int s = 0; s < kFullSlots; ++s) {
-                    const uint32_t p = block_byte(w, 2 + s);
+                    const uint32_t p = block_byte(w[c], 2 + s);
                     const uint32_t hi = (p * 57u) >> 9;
                     const uint32_t lo = p - 9u * hi;
 #pragma unroll
-                    for (int j = 0; j < BT; ++j) {
-                        const float *L = lut + (j * sub_groups + gi) * kLutFloats;
-                        sum[j] += L[s * kL2Entries + lo] + L[kL3Base + s * kL3Entries + hi];
-                    }
+                    for (int j = 0; j < BT; ++j)
+                        sum[j] += lut[j][c][s * kL2Entries + lo] + lut[j][c][kL3Base + s * kL3Entries + hi];
                 }
-                const uint32_t tail = min(w[6] >> 24, kMaxTailByte);
+                const uint32_t tail = min(w[c][6] >> 24, kMaxTailByte);
 #pragma unroll
                 for (int j = 0; j < BT; ++j) {
-                    sum[j] += lut[(j * sub_groups + gi) * kLutFloats + kTailBase + tail];
+                    sum[j] += lut[j][c][kTailBase + tail];
                     acc[j] = fmaf(scale, sum[j], acc[j]);
                 }
-#pragma unroll
-                for (int k = 0; k < kBlockWords; ++k) w[k] = nw[k];
             }
         }
     }
 
-    if (row < N) {
+    // 4. Output.
+    if (k_split == 1) {
+        if (row_ok) {
+#pragma unroll
+            for (int j = 0; j < BT; ++j)
+                if (b0 + j < M) y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(acc[j]);
+        }
+        return;
+    }
+    if (row_ok) {
+#pragma unroll
+        for (int j = 0; j < BT; ++j)
+            if (b0 + j < M) partial[(static_cast<int64_t>(blockIdx.z) * M + b0 + j) * N + row] = acc[j];
+    }
+    __threadfence();
+    __syncthreads();
+    unsigned *counter = counters + static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    if (tid == 0) s_last = atomicAdd(counter, 1u) == static_cast<unsigned>(k_split - 1);
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    if (row_ok) {
 #pragma unroll
         for (int j = 0; j < BT; ++j) {
-            const int sample = batch0 + j;
-            if (sample < M) {
-                if (partial)
-                    partial[(static_cast<int64_t>(chunk) * M + sample) * N + row] = acc[j];
-                else
-                    y[static_cast<int64_t>(sample) * N + row] = from_f32<T>(acc[j]);
-            }
+            if (b0 + j >= M) continue;
+            const float *src = partial + static_cast<int64_t>(b0 + j) * N + row;
+            const int64_t stride = static_cast<int64_t>(M) * N;
+            float a = __builtin_nontemporal_load(src);
+            for (int z = 1; z < k_split; ++z) a += __builtin_nontemporal_load(src + z * stride);
+            y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(a);
         }
     }
+    if (tid == 0) atomicExch(counter, 0u);
 }
 
 template <typename T>
@@ -386,11 +456,11 @@ __global__ __launch_bounds__(kThreads) void reduce_partials_kernel(const float *
 //
 // Workgroup tile 128 (M) x 128 (N), one 128-weight group per K step. Each K
 // step stages the activation tile (fp16, straight copy) and decodes the weight
-// tile -- 128 rows x one 28-byte block -- into fp16 (t - 1) * scale in LDS
-// (exact in fp16, so the only rounding is the fp32 accumulation). Four waves
-// in a 2 x 2 grid each own 64 x 64 outputs = 2 x 2 tiles of
-// v_mfma_f32_32x32x16_f16. LDS rows are padded by 8 halves so the 16-byte
-// fragment reads of a wave fall in distinct banks.
+// tile -- 128 rows x one block, read as seven coalesced words per row -- into
+// fp16 (t - 1) * scale in LDS (exact in fp16, so the only rounding is the fp32
+// accumulation). Four waves in a 2 x 2 grid each own 64 x 64 outputs = 2 x 2
+// tiles of v_mfma_f32_32x32x16_f16. LDS rows are padded by 8 halves so the
+// 16-byte fragment reads of a wave fall in distinct banks.
 // ---------------------------------------------------------------------------
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
@@ -415,7 +485,7 @@ __device__ __forceinline__ void decode_half_block(const uint32_t (&w)[kBlockWord
 }
 
 __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
-    const uint8_t *__restrict__ blocks, const _Float16 *__restrict__ x, _Float16 *__restrict__ y,
+    const uint32_t *__restrict__ packed, const _Float16 *__restrict__ x, _Float16 *__restrict__ y,
     float *__restrict__ partial, int M, int N, int G, int chunk_groups) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[kGemmBM * kGemmStride];
     __shared__ __attribute__((aligned(16))) _Float16 ws[kGemmBN * kGemmStride];
@@ -440,8 +510,9 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int dec_row = tid >> 1;
-    const int dec_half = tid & 1;
+    // Decoder assignment: lanes own consecutive rows (coalesced word loads).
+    const int dec_row = tid & (kGemmBN - 1);
+    const int dec_half = tid / kGemmBN;
     const int dec_n = n0 + dec_row;
 
     for (int g = g_begin; g < g_end; ++g) {
@@ -466,11 +537,11 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
         {
             _Float16 wv[64];
             if (dec_n < N) {
-                const uint32_t *bp = reinterpret_cast<const uint32_t *>(blocks) +
-                                     (static_cast<int64_t>(dec_n) * G + g) * kBlockWords;
                 uint32_t w[kBlockWords];
+                const uint32_t *p = packed + (static_cast<int64_t>(dec_n / kTileRows) * G + g) * kTileGroupWords +
+                                    (dec_n % kTileRows);
 #pragma unroll
-                for (int k = 0; k < kBlockWords; ++k) w[k] = bp[k];
+                for (int j = 0; j < kBlockWords; ++j) w[j] = p[j * kTileRows];
                 const float scale = half_bits_to_float(w[0]);
                 if (dec_half == 0)
                     decode_half_block<0>(w, scale, wv);
@@ -529,17 +600,10 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 // ---------------------------------------------------------------------------
 // Host-side geometry
 // ---------------------------------------------------------------------------
-// Workgroups a split is sized to reach: a few per CU on the 256-CU part.
-constexpr int64_t kSplitTargetWorkgroups = 1024;
-constexpr int kLutMaxBytes = 64 * 1024;
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-int largest_split(int64_t groups_per_row, int64_t workgroups) {
-    int64_t budget = kSplitTargetWorkgroups / (workgroups > 0 ? workgroups : 1);
-    if (budget < 1) budget = 1;
-    if (budget > groups_per_row) budget = groups_per_row;
-    for (int64_t k = budget; k > 1; --k)
-        if (groups_per_row % k == 0) return static_cast<int>(k);
-    return 1;
+int64_t packed_words(int64_t rows, int64_t columns) {
+    return ceil_div(rows, kTileRows) * (columns / kBlockWeights) * kTileGroupWords;
 }
 
 int check_dtype(int dtype) {
@@ -556,19 +620,36 @@ int check_geometry(int64_t M, int64_t rows, int64_t columns) {
         return fail(TERNEL_TQ1_EINVAL, "%lld columns is not a multiple of the 128-weight group",
                     static_cast<long long>(columns));
     if (M <= 0) return fail(TERNEL_TQ1_EINVAL, "activations have an empty batch dimension");
-    if (rows > INT32_MAX || M > INT32_MAX || columns / kBlockWeights > INT32_MAX)
+    if (rows > INT32_MAX - kThreads || M > INT32_MAX || columns / kBlockWeights > INT32_MAX / kTileGroupWords)
         return fail(TERNEL_TQ1_EINVAL, "tensor too large for 32-bit row/batch indices");
     return TERNEL_TQ1_OK;
 }
 
+// Workgroups a K split is sized to reach: a few resident per CU on the 256-CU part.
+constexpr int64_t kLutTargetWorkgroups = 512;
+
+// The split-K workspace starts with a fixed region of arrival counters, one per
+// (row block, batch tile), that is all-zero between calls. Fixing its size keeps
+// that true when one workspace serves calls of different shapes: partials are
+// always written past it.
+constexpr int kCounterSlots = 16384;
+constexpr size_t kCounterRegionBytes = kCounterSlots * sizeof(unsigned);
+
 struct LutPlan {
     int batch_tile;
+    int chunk;         // groups per sub-chunk (compile-time C)
+    int chunk_groups;  // groups per workgroup, a multiple of chunk
     int k_split;
-    int chunk_groups;
-    int sub_groups;
-    int64_t tiles;
+    int64_t row_blocks;
     int64_t batch_tiles;
+    size_t counter_bytes;
+    size_t partial_bytes;
 };
+
+bool lut_chunk_supported(int batch_tile, int chunk) {
+    if (batch_tile == 4) return chunk == 1 || chunk == 2 || chunk == 4;
+    return chunk == 1 || chunk == 2 || chunk == 4 || chunk == 8;
+}
 
 int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split, LutPlan *plan) {
     const int64_t G = columns / kBlockWeights;
@@ -576,60 +657,86 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
     if (batch_tile != 1 && batch_tile != 2 && batch_tile != 4)
         return fail(TERNEL_TQ1_EINVAL, "batch tile must be 1, 2 or 4, got %d", batch_tile);
     plan->batch_tile = batch_tile;
-    plan->tiles = (rows + kThreads - 1) / kThreads;
-    plan->batch_tiles = (M + batch_tile - 1) / batch_tile;
+    plan->row_blocks = ceil_div(rows, kThreads);
+    plan->batch_tiles = ceil_div(M, batch_tile);
     if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
-    if (k_split == 0) k_split = largest_split(G, plan->tiles * plan->batch_tiles);
-    if (G % k_split)
-        return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row",
-                    k_split, static_cast<long long>(G));
-    plan->k_split = k_split;
-    plan->chunk_groups = static_cast<int>(G / k_split);
-    const int cap = kLutMaxBytes / (batch_tile * kLutFloats * 4);
-    int sub = plan->chunk_groups;
-    if (sub > cap) {
-        // Equal sub-chunks no larger than the LDS cap.
-        const int pieces = (plan->chunk_groups + cap - 1) / cap;
-        sub = (plan->chunk_groups + pieces - 1) / pieces;
+    if (k_split > 0 && G % k_split)
+        return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row", k_split,
+                    static_cast<long long>(G));
+    if (k_split > 0) {
+        // A requested split fixes the groups per workgroup; they are walked in
+        // sub-chunks of the largest compiled size that divides them, in order,
+        // so a split of one keeps the reference's exact summation order.
+        plan->chunk_groups = static_cast<int>(G / k_split);
+        int c = 1;
+        for (int cand : {8, 4, 2, 1})
+            if (plan->chunk_groups % cand == 0 && lut_chunk_supported(batch_tile, cand)) {
+                c = cand;
+                break;
+            }
+        plan->chunk = c;
+        plan->k_split = k_split;
+    } else {
+        // Largest compiled chunk that still offers the target number of workgroups.
+        int c = 1;
+        for (int cand : {8, 4, 2}) {
+            if (!lut_chunk_supported(batch_tile, cand) || G % cand) continue;
+            if (plan->row_blocks * plan->batch_tiles * (G / cand) >= kLutTargetWorkgroups) {
+                c = cand;
+                break;
+            }
+        }
+        plan->chunk = c;
+        plan->chunk_groups = c;
+        plan->k_split = static_cast<int>(G / c);
     }
-    plan->sub_groups = sub;
+    if (plan->k_split > 65535) return fail(TERNEL_TQ1_EINVAL, "K too large for one launch");
+    if (plan->k_split > 1 && plan->row_blocks * plan->batch_tiles > kCounterSlots)
+        return fail(TERNEL_TQ1_EINVAL, "%lld row blocks x %lld batch tiles exceed the %d split-K counters",
+                    static_cast<long long>(plan->row_blocks), static_cast<long long>(plan->batch_tiles),
+                    kCounterSlots);
+    plan->counter_bytes = plan->k_split > 1 ? kCounterRegionBytes : 0;
+    plan->partial_bytes =
+        plan->k_split > 1 ? static_cast<size_t>(plan->k_split) * static_cast<size_t>(M) * rows * sizeof(float) : 0;
     return TERNEL_TQ1_OK;
 }
 
-template <typename T>
-int launch_lut(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows,
-               int64_t columns, const LutPlan &plan, float *partial, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(plan.tiles), static_cast<unsigned>(plan.batch_tiles),
+template <typename T, int C, int BT>
+void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *x, void *y, float *partial,
+                       unsigned *counters, int64_t M, int64_t rows, int G, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.batch_tiles),
                     static_cast<unsigned>(plan.k_split));
-    const size_t lds = static_cast<size_t>(plan.batch_tile) * plan.sub_groups * kLutFloats * 4;
+    hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT>), grid, dim3(kThreads), 0, stream, packed,
+                       static_cast<const T *>(x), static_cast<T *>(y), partial, counters, static_cast<int>(M),
+                       static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
+}
+
+template <typename T>
+int launch_lut(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+               const LutPlan &plan, void *ws, hipStream_t stream) {
     const int G = static_cast<int>(columns / kBlockWeights);
-    const T *xt = static_cast<const T *>(x);
-    T *yt = static_cast<T *>(y);
-    switch (plan.batch_tile) {
-        case 1:
-            hipLaunchKernelGGL((lut_matmul_kernel<T, 1>), grid, dim3(kThreads), lds, stream, blocks, xt, yt,
-                               partial, static_cast<int>(M), static_cast<int>(rows), G,
-                               plan.chunk_groups, plan.sub_groups);
-            break;
-        case 2:
-            hipLaunchKernelGGL((lut_matmul_kernel<T, 2>), grid, dim3(kThreads), lds, stream, blocks, xt, yt,
-                               partial, static_cast<int>(M), static_cast<int>(rows), G,
-                               plan.chunk_groups, plan.sub_groups);
-            break;
-        default:
-            hipLaunchKernelGGL((lut_matmul_kernel<T, 4>), grid, dim3(kThreads), lds, stream, blocks, xt, yt,
-                               partial, static_cast<int>(M), static_cast<int>(rows), G,
-                               plan.chunk_groups, plan.sub_groups);
-            break;
+    unsigned *counters = plan.k_split > 1 ? static_cast<unsigned *>(ws) : nullptr;
+    float *partial =
+        plan.k_split > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + plan.counter_bytes) : nullptr;
+#define TQ1_LUT_CASE(CC, BB)                                                                         \
+    if (plan.chunk == CC && plan.batch_tile == BB) {                                                 \
+        launch_lut_kernel<T, CC, BB>(plan, packed, x, y, partial, counters, M, rows, G, stream);     \
+        TQ1_LAUNCH_CHECK();                                                                          \
+        return TERNEL_TQ1_OK;                                                                        \
     }
-    TQ1_LAUNCH_CHECK();
-    if (partial) {
-        const int64_t count = M * rows;
-        hipLaunchKernelGGL((reduce_partials_kernel<T>), dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads)),
-                           dim3(kThreads), 0, stream, partial, yt, count, plan.k_split);
-        TQ1_LAUNCH_CHECK();
-    }
-    return TERNEL_TQ1_OK;
+    TQ1_LUT_CASE(1, 1)
+    TQ1_LUT_CASE(2, 1)
+    TQ1_LUT_CASE(4, 1)
+    TQ1_LUT_CASE(8, 1)
+    TQ1_LUT_CASE(1, 2)
+    TQ1_LUT_CASE(2, 2)
+    TQ1_LUT_CASE(4, 2)
+    TQ1_LUT_CASE(8, 2)
+    TQ1_LUT_CASE(1, 4)
+    TQ1_LUT_CASE(2, 4)
+    TQ1_LUT_CASE(4, 4)
+#undef TQ1_LUT_CASE
+    return fail(TERNEL_TQ1_EINVAL, "no LUT23 kernel for chunk %d, batch tile %d", plan.chunk, plan.batch_tile);
 }
 
 struct GemmPlan {
@@ -639,40 +746,45 @@ struct GemmPlan {
     int64_t m_tiles;
 };
 
+int largest_divisor_split(int64_t groups_per_row, int64_t workgroups, int64_t target) {
+    int64_t budget = target / (workgroups > 0 ? workgroups : 1);
+    if (budget < 1) budget = 1;
+    if (budget > groups_per_row) budget = groups_per_row;
+    for (int64_t k = budget; k > 1; --k)
+        if (groups_per_row % k == 0) return static_cast<int>(k);
+    return 1;
+}
+
 int plan_gemm(int64_t M, int64_t rows, int64_t columns, int k_split, GemmPlan *plan) {
     const int64_t G = columns / kBlockWeights;
-    plan->n_tiles = (rows + kGemmBN - 1) / kGemmBN;
-    plan->m_tiles = (M + kGemmBM - 1) / kGemmBM;
+    plan->n_tiles = ceil_div(rows, kGemmBN);
+    plan->m_tiles = ceil_div(M, kGemmBM);
     if (plan->m_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");
     if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
     if (k_split == 0) {
         const int64_t wgs = plan->n_tiles * plan->m_tiles;
-        k_split = wgs >= 512 ? 1 : largest_split(G, wgs * 2 > 0 ? wgs * 2 : 1);
-        // largest_split targets kSplitTargetWorkgroups; halve the ambition for
-        // the MFMA kernel, whose workgroups are heavier.
+        k_split = wgs >= 512 ? 1 : largest_divisor_split(G, wgs, 512);
     }
     if (G % k_split)
-        return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row",
-                    k_split, static_cast<long long>(G));
+        return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row", k_split,
+                    static_cast<long long>(G));
     plan->k_split = k_split;
     plan->chunk_groups = static_cast<int>(G / k_split);
     return TERNEL_TQ1_OK;
 }
 
-int launch_gemm(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows,
-                int64_t columns, const GemmPlan &plan, float *partial, hipStream_t stream) {
+int launch_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+                const GemmPlan &plan, float *partial, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(plan.n_tiles), static_cast<unsigned>(plan.m_tiles),
                     static_cast<unsigned>(plan.k_split));
-    hipLaunchKernelGGL(mfma_gemm_kernel, grid, dim3(kThreads), 0, stream, blocks,
-                       static_cast<const _Float16 *>(x), static_cast<_Float16 *>(y), partial,
-                       static_cast<int>(M), static_cast<int>(rows),
-                       static_cast<int>(columns / kBlockWeights), plan.chunk_groups);
+    hipLaunchKernelGGL(mfma_gemm_kernel, grid, dim3(kThreads), 0, stream, packed,
+                       static_cast<const _Float16 *>(x), static_cast<_Float16 *>(y), partial, static_cast<int>(M),
+                       static_cast<int>(rows), static_cast<int>(columns / kBlockWeights), plan.chunk_groups);
     TQ1_LAUNCH_CHECK();
     if (partial) {
         const int64_t count = M * rows;
-        hipLaunchKernelGGL((reduce_partials_kernel<_Float16>),
-                           dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                           stream, partial, static_cast<_Float16 *>(y), count, plan.k_split);
+        hipLaunchKernelGGL((reduce_partials_kernel<_Float16>), dim3(static_cast<unsigned>(ceil_div(count, kThreads))),
+                           dim3(kThreads), 0, stream, partial, static_cast<_Float16 *>(y), count, plan.k_split);
         TQ1_LAUNCH_CHECK();
     }
     return TERNEL_TQ1_OK;
@@ -681,6 +793,12 @@ int launch_gemm(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_
 // The dispatch rule of packed_matmul, retuned for MI355X: the LUT23 kernel up
 // to this many activation rows, the MFMA kernel above it (fp16 only).
 constexpr int64_t kLinearLutMaxBatch = 4;
+
+int check_packed_pointer(const void *packed) {
+    if (!packed) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (reinterpret_cast<uintptr_t>(packed) & 3u) return fail(TERNEL_TQ1_EINVAL, "packed weights must be 4-byte aligned");
+    return TERNEL_TQ1_OK;
+}
 
 }  // namespace
 
@@ -691,21 +809,26 @@ extern "C" {
 
 const char *ternel_tq1_last_error(void) { return g_last_error; }
 
-const char *ternel_tq1_version(void) { return "ternel-tq1-gfx950 0.1.0"; }
+const char *ternel_tq1_version(void) { return "ternel-tq1-gfx950 0.2.0"; }
+
+int64_t ternel_tq1_packed_words(int64_t rows, int64_t columns) {
+    if (rows <= 0 || columns <= 0 || columns % kBlockWeights) return 0;
+    return packed_words(rows, columns);
+}
 
 int ternel_tq1_validate(const uint8_t *blocks, int64_t nblocks, uint64_t *counters, void *stream) {
     g_last_error[0] = '\0';
-    if (!blocks || !counters) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (!counters) return fail(TERNEL_TQ1_EINVAL, "null pointer");
     if (nblocks < 0) return fail(TERNEL_TQ1_EINVAL, "negative block count");
-    if (reinterpret_cast<uintptr_t>(blocks) & 3u)
-        return fail(TERNEL_TQ1_EINVAL, "blocks must be 4-byte aligned");
+    if (nblocks > 0 && !blocks) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (reinterpret_cast<uintptr_t>(blocks) & 3u) return fail(TERNEL_TQ1_EINVAL, "blocks must be 4-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     auto *cnt = reinterpret_cast<unsigned long long *>(counters);
     hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(64), 0, s, cnt, 2);
     TQ1_LAUNCH_CHECK();
     if (nblocks == 0) return TERNEL_TQ1_OK;
     const int64_t nwords = nblocks * kBlockWords;
-    int64_t grid = (nwords + kThreads * 4 - 1) / (kThreads * 4);
+    int64_t grid = ceil_div(nwords, kThreads * 4);
     if (grid > 8192) grid = 8192;
     hipLaunchKernelGGL(validate_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
                        reinterpret_cast<const uint32_t *>(blocks), nwords, cnt);
@@ -716,11 +839,10 @@ int ternel_tq1_validate(const uint8_t *blocks, int64_t nblocks, uint64_t *counte
 int ternel_tq1_decode(const uint8_t *blocks, int64_t nblocks, uint8_t *scales_out, uint8_t *codes_out,
                       void *stream) {
     g_last_error[0] = '\0';
-    if (!blocks || !scales_out || !codes_out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
     if (nblocks < 0) return fail(TERNEL_TQ1_EINVAL, "negative block count");
     if (nblocks == 0) return TERNEL_TQ1_OK;
-    const int64_t threads = nblocks * kCodeSlots;
-    const int64_t grid = (threads + kThreads - 1) / kThreads;
+    if (!blocks || !scales_out || !codes_out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    const int64_t grid = ceil_div(nblocks * kCodeSlots, kThreads);
     if (grid > INT32_MAX) return fail(TERNEL_TQ1_EINVAL, "too many blocks for one decode launch");
     hipLaunchKernelGGL(decode_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
                        static_cast<hipStream_t>(stream), blocks, nblocks, scales_out, codes_out);
@@ -728,43 +850,66 @@ int ternel_tq1_decode(const uint8_t *blocks, int64_t nblocks, uint8_t *scales_ou
     return TERNEL_TQ1_OK;
 }
 
-size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int batch_tile,
-                                         int k_split) {
+int ternel_tq1_interleave(const uint8_t *blocks, int64_t rows, int64_t columns, uint32_t *packed, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(1, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if (!blocks || !packed) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(blocks) | reinterpret_cast<uintptr_t>(packed)) & 3u)
+        return fail(TERNEL_TQ1_EINVAL, "blocks and packed weights must be 4-byte aligned");
+    const int64_t total = packed_words(rows, columns);
+    hipLaunchKernelGGL(interleave_kernel, dim3(static_cast<unsigned>(ceil_div(total, kThreads))), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), reinterpret_cast<const uint32_t *>(blocks), packed, rows,
+                       columns / kBlockWeights, total);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+int ternel_tq1_deinterleave(const uint32_t *packed, int64_t rows, int64_t columns, uint8_t *blocks, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(1, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if (!blocks || !packed) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(blocks) | reinterpret_cast<uintptr_t>(packed)) & 3u)
+        return fail(TERNEL_TQ1_EINVAL, "blocks and packed weights must be 4-byte aligned");
+    const int64_t total = rows * (columns / kBlockWeights) * kBlockWords;
+    hipLaunchKernelGGL(deinterleave_kernel, dim3(static_cast<unsigned>(ceil_div(total, kThreads))), dim3(kThreads),
+                       0, static_cast<hipStream_t>(stream), packed, reinterpret_cast<uint32_t *>(blocks),
+                       columns / kBlockWeights, total);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
     LutPlan plan;
     if (plan_lut(M, rows, columns, batch_tile, k_split, &plan) != TERNEL_TQ1_OK) return 0;
-    return plan.k_split > 1 ? static_cast<size_t>(plan.k_split) * M * rows * sizeof(float) : 0;
+    return plan.counter_bytes + plan.partial_bytes;
 }
 
-int ternel_tq1_matmul(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows,
-                      int64_t columns, int dtype, int batch_tile, int k_split, void *ws, size_t ws_bytes,
-                      void *stream) {
+int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+                      int dtype, int batch_tile, int k_split, void *ws, size_t ws_bytes, void *stream) {
     g_last_error[0] = '\0';
     int rc;
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
-    if (!blocks || !x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
-    if (reinterpret_cast<uintptr_t>(blocks) & 3u)
-        return fail(TERNEL_TQ1_EINVAL, "blocks must be 4-byte aligned");
     LutPlan plan;
     if ((rc = plan_lut(M, rows, columns, batch_tile, k_split, &plan)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+    if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
     if (plan.batch_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");
-    float *partial = nullptr;
-    if (plan.k_split > 1) {
-        const size_t need = static_cast<size_t>(plan.k_split) * M * rows * sizeof(float);
-        if (!ws || ws_bytes < need)
-            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs",
-                        ws_bytes, need);
-        partial = static_cast<float *>(ws);
-    }
+    const size_t need = plan.counter_bytes + plan.partial_bytes;
+    if (need && (!ws || ws_bytes < need))
+        return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
+                    need);
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (dtype) {
         case TERNEL_TQ1_F16:
-            return launch_lut<_Float16>(blocks, x, y, M, rows, columns, plan, partial, s);
+            return launch_lut<_Float16>(packed, x, y, M, rows, columns, plan, ws, s);
         case TERNEL_TQ1_BF16:
-            return launch_lut<bf16_t>(blocks, x, y, M, rows, columns, plan, partial, s);
+            return launch_lut<bf16_t>(packed, x, y, M, rows, columns, plan, ws, s);
         default:
-            return launch_lut<float>(blocks, x, y, M, rows, columns, plan, partial, s);
+            return launch_lut<float>(packed, x, y, M, rows, columns, plan, ws, s);
     }
 }
 
@@ -772,57 +917,60 @@ size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns,
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
     GemmPlan plan;
     if (plan_gemm(M, rows, columns, k_split, &plan) != TERNEL_TQ1_OK) return 0;
-    return plan.k_split > 1 ? static_cast<size_t>(plan.k_split) * M * rows * sizeof(float) : 0;
+    return plan.k_split > 1 ? kCounterRegionBytes + static_cast<size_t>(plan.k_split) * M * rows * sizeof(float)
+                            : 0;
 }
 
-int ternel_tq1_gemm(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
                     int dtype, int k_split, void *ws, size_t ws_bytes, void *stream) {
     g_last_error[0] = '\0';
     int rc;
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if (dtype != TERNEL_TQ1_F16)
         return fail(TERNEL_TQ1_EINVAL, "the MFMA path takes fp16 activations, got dtype code %d", dtype);
-    if (!blocks || !x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
-    if ((reinterpret_cast<uintptr_t>(blocks) & 3u) || (reinterpret_cast<uintptr_t>(x) & 15u))
-        return fail(TERNEL_TQ1_EINVAL, "blocks must be 4-byte and activations 16-byte aligned");
     GemmPlan plan;
     if ((rc = plan_gemm(M, rows, columns, k_split, &plan)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+    if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (reinterpret_cast<uintptr_t>(x) & 15u) return fail(TERNEL_TQ1_EINVAL, "activations must be 16-byte aligned");
     float *partial = nullptr;
     if (plan.k_split > 1) {
-        const size_t need = static_cast<size_t>(plan.k_split) * M * rows * sizeof(float);
+        // Partials go past the counter region, which stays untouched (and zero).
+        const size_t need = kCounterRegionBytes + static_cast<size_t>(plan.k_split) * M * rows * sizeof(float);
         if (!ws || ws_bytes < need)
-            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs",
-                        ws_bytes, need);
-        partial = static_cast<float *>(ws);
+            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
+                        need);
+        partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes);
     }
-    return launch_gemm(blocks, x, y, M, rows, columns, plan, partial, static_cast<hipStream_t>(stream));
+    return launch_gemm(packed, x, y, M, rows, columns, plan, partial, static_cast<hipStream_t>(stream));
 }
 
-int ternel_tq1_get_rows(const uint8_t *blocks, int64_t rows, int64_t columns, const int64_t *ids,
-                        int64_t n_ids, void *out, int dtype, void *stream) {
+int ternel_tq1_get_rows(const uint32_t *packed, int64_t rows, int64_t columns, const int64_t *ids, int64_t n_ids,
+                        void *out, int dtype, void *stream) {
     g_last_error[0] = '\0';
     int rc;
     if ((rc = check_geometry(1, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
     if (n_ids <= 0) return fail(TERNEL_TQ1_EINVAL, "indices are empty");
-    if (!blocks || !ids || !out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+    if (!ids || !out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
     const int G = static_cast<int>(columns / kBlockWeights);
     const int per_token = G * kCodeSlots;
-    const dim3 grid(static_cast<unsigned>((per_token + kThreads - 1) / kThreads),
+    const dim3 grid(static_cast<unsigned>(ceil_div(per_token, kThreads)),
                     static_cast<unsigned>(n_ids < 65535 ? n_ids : 65535));
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (dtype) {
         case TERNEL_TQ1_F16:
-            hipLaunchKernelGGL((get_rows_kernel<_Float16>), grid, dim3(kThreads), 0, s, blocks, rows, G, ids,
-                               n_ids, static_cast<_Float16 *>(out));
+            hipLaunchKernelGGL((get_rows_kernel<_Float16>), grid, dim3(kThreads), 0, s, packed, rows, G, ids, n_ids,
+                               static_cast<_Float16 *>(out));
             break;
         case TERNEL_TQ1_BF16:
-            hipLaunchKernelGGL((get_rows_kernel<bf16_t>), grid, dim3(kThreads), 0, s, blocks, rows, G, ids,
-                               n_ids, static_cast<bf16_t *>(out));
+            hipLaunchKernelGGL((get_rows_kernel<bf16_t>), grid, dim3(kThreads), 0, s, packed, rows, G, ids, n_ids,
+                               static_cast<bf16_t *>(out));
             break;
         default:
-            hipLaunchKernelGGL((get_rows_kernel<float>), grid, dim3(kThreads), 0, s, blocks, rows, G, ids,
-                               n_ids, static_cast<float *>(out));
+            hipLaunchKernelGGL((get_rows_kernel<float>), grid, dim3(kThreads), 0, s, packed, rows, G, ids, n_ids,
+                               static_cast<float *>(out));
             break;
     }
     TQ1_LAUNCH_CHECK();
@@ -835,11 +983,11 @@ size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t column
     return ternel_tq1_gemm_workspace_bytes(M, rows, columns, 0);
 }
 
-int ternel_tq1_linear(const uint8_t *blocks, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
                       int dtype, void *ws, size_t ws_bytes, void *stream) {
     if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
-        return ternel_tq1_matmul(blocks, x, y, M, rows, columns, dtype, 0, 0, ws, ws_bytes, stream);
-    return ternel_tq1_gemm(blocks, x, y, M, rows, columns, dtype, 0, ws, ws_bytes, stream);
+        return ternel_tq1_matmul(packed, x, y, M, rows, columns, dtype, 0, 0, ws, ws_bytes, stream);
+    return ternel_tq1_gemm(packed, x, y, M, rows, columns, dtype, 0, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

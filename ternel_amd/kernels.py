@@ -1,12 +1,17 @@
 """Functional entry points over the gfx950 library (mirror of src/ternel_mlx/kernels.py:951-1398).
 
-``tq1_matmul`` (LUT23, decode GEMV and small batches), ``tq1_gemm`` (MFMA,
-prefill) and ``tq1_get_rows`` (embedding gather) take canonical device blocks
-``(rows, groups_per_row, 28)`` uint8, check every argument on the host and raise
-``FormatError`` *before* anything is launched, exactly as the reference's
-wrappers do (``_check_packed``/``_check_activations``, kernels.py:1191-1212,
-1274-1284). Outputs are fresh tensors in the activation dtype; split-K
-workspaces are allocated here by torch and handed to the C ABI.
+``tq1_matmul`` (LUT23: decode GEMV and small batches), ``tq1_gemm`` (MFMA:
+prefill) and ``tq1_get_rows`` (embedding gather) take the *packed* device
+weight -- the canonical 28-byte blocks permuted into 64-row word-interleaved
+tiles, a uint32 tensor of shape ``(ceil(rows/64), groups_per_row, 7, 64)`` made
+by :func:`pack_weights` -- check every argument on the host and raise
+``FormatError`` before anything is launched, as the reference's wrappers do
+(``_check_packed``/``_check_activations``, kernels.py:1191-1212, 1274-1284).
+Outputs are fresh tensors in the activation dtype.
+
+Split-K workspaces: the LUT23 kernel reduces its K chunks inside the launch
+through arrival counters that must start at zero and are left at zero, so the
+workspace is allocated zero-filled once per (device, stream) and reused.
 """
 
 from __future__ import annotations
@@ -17,13 +22,14 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .format import BLOCK_BYTES, BLOCK_SIZE, FormatError
+from .format import BLOCK_BYTES, FormatError, as_device_blocks
 from .layout import PackedTensorLayout
 
 ACTIVATION_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 _DTYPE_CODE = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
 
-# One thread per output row in a 256-lane workgroup (4 wave64s).
+TILE_ROWS = 64
+BLOCK_WORDS = 7
 LUT23_THREADS = 256
 LUT23_BATCH_TILES = (1, 2, 4)
 
@@ -32,8 +38,8 @@ LUT23_BATCH_TILES = (1, 2, 4)
 class MatmulConfig:
     """LUT23 knobs (src/ternel_mlx/kernels.py:963-1006): batch tile and K split.
 
-    ``k_split=0`` lets the library pick the largest divisor of the group count
-    that keeps the grid near its MI355X workgroup target.
+    ``0`` means automatic: the batch tile follows the batch (1, 2 or 4) and the
+    split the largest chunk that still fills the 256 CUs.
     """
 
     batch_tile: int = 0
@@ -70,22 +76,45 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def check_blocks(blocks: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
-    """Device canonical blocks of ``layout``'s shape, or FormatError."""
-    if not isinstance(blocks, torch.Tensor):
-        raise FormatError("blocks must be a torch tensor on the GPU")
-    if blocks.dtype != torch.uint8:
-        raise FormatError(f"blocks must be uint8, got {blocks.dtype}")
-    expected = layout.canonical_shape
-    if tuple(blocks.shape) != expected and not (blocks.ndim == 2 and tuple(blocks.shape) == (layout.groups, BLOCK_BYTES)):
-        raise FormatError(f"blocks shape {tuple(blocks.shape)} does not match {expected}")
-    if not blocks.is_cuda:
-        raise FormatError("blocks must live on the GPU")
-    if not blocks.is_contiguous():
-        raise FormatError("blocks must be contiguous")
-    if blocks.data_ptr() % 4:
-        raise FormatError("blocks must be 4-byte aligned")
+def packed_shape(layout: PackedTensorLayout) -> tuple[int, int, int, int]:
+    return (math.ceil(layout.rows / TILE_ROWS), layout.groups_per_row, BLOCK_WORDS, TILE_ROWS)
+
+
+def pack_weights(blocks, *, layout: PackedTensorLayout) -> torch.Tensor:
+    """Canonical blocks (host or device) -> packed device words (exact permutation)."""
+    device_blocks = as_device_blocks(blocks)
+    if device_blocks.shape[0] != layout.groups:
+        raise FormatError(
+            f"expected {layout.groups} blocks for {layout.rows}x{layout.columns}, got {device_blocks.shape[0]}"
+        )
+    packed = torch.empty(packed_shape(layout), dtype=torch.int32, device=device_blocks.device)
+    assert packed.numel() == _lib.lib().ternel_tq1_packed_words(layout.rows, layout.columns)
+    _lib.check(_lib.lib().ternel_tq1_interleave(device_blocks.data_ptr(), layout.rows, layout.columns,
+                                                packed.data_ptr(), _stream(device_blocks.device)))
+    return packed
+
+
+def unpack_weights(packed: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+    """Packed device words -> canonical ``(rows, G, 28)`` uint8 device blocks."""
+    check_packed(packed, layout=layout)
+    blocks = torch.empty(layout.canonical_shape, dtype=torch.uint8, device=packed.device)
+    _lib.check(_lib.lib().ternel_tq1_deinterleave(packed.data_ptr(), layout.rows, layout.columns,
+                                                  blocks.data_ptr(), _stream(packed.device)))
     return blocks
+
+
+def check_packed(packed: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+    if not isinstance(packed, torch.Tensor):
+        raise FormatError("packed weights must be a torch tensor on the GPU")
+    if packed.dtype not in (torch.int32, torch.uint32):
+        raise FormatError(f"packed weights must be 32-bit words, got {packed.dtype}")
+    if tuple(packed.shape) != packed_shape(layout):
+        raise FormatError(f"packed weights of shape {tuple(packed.shape)} do not match {packed_shape(layout)}")
+    if not packed.is_cuda:
+        raise FormatError("packed weights must live on the GPU")
+    if not packed.is_contiguous():
+        raise FormatError("packed weights must be contiguous")
+    return packed
 
 
 def check_activations(x: torch.Tensor, *, layout: PackedTensorLayout) -> int:
@@ -103,7 +132,26 @@ def check_activations(x: torch.Tensor, *, layout: PackedTensorLayout) -> int:
     return x.shape[0]
 
 
-def tq1_matmul(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Zero-initialised scratch for split-K, one per (device, stream), grown on demand.
+
+    The LUT23 kernel leaves its arrival counters at zero after every launch, so
+    the buffer only needs zeroing when it is created.
+    """
+    if nbytes == 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(), _stream(device))
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+def tq1_matmul(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
                config: MatmulConfig | None = None) -> torch.Tensor:
     """``x @ W.T`` through the LUT23 kernel; ``(batch, rows)`` in ``x.dtype``.
 
@@ -111,7 +159,7 @@ def tq1_matmul(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLay
     does not divide the group count is refused, as there.
     """
     config = config or MatmulConfig()
-    check_blocks(blocks, layout=layout)
+    check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
     if config.k_split and layout.groups_per_row % config.k_split:
         raise FormatError(
@@ -122,19 +170,19 @@ def tq1_matmul(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLay
     handle = _lib.lib()
     need = handle.ternel_tq1_matmul_workspace_bytes(batch, layout.rows, layout.columns,
                                                      config.batch_tile, config.k_split)
-    ws = torch.empty(max(need, 4), dtype=torch.uint8, device=x.device) if need else None
+    ws = workspace(x.device, need)
     _lib.check(handle.ternel_tq1_matmul(
-        blocks.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns,
+        packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns,
         _DTYPE_CODE[x.dtype], config.batch_tile, config.k_split,
-        ws.data_ptr() if ws is not None else None, need, _stream(x.device)))
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(x.device)))
     return out
 
 
-def tq1_gemm(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
+def tq1_gemm(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
              config: GemmConfig | None = None) -> torch.Tensor:
     """``x @ W.T`` on the MFMA kernel (fp16 activations); reference tq1_gemm, kernels.py:1287-1357."""
     config = config or GemmConfig()
-    check_blocks(blocks, layout=layout)
+    check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
     if x.dtype != torch.float16:
         raise FormatError(f"the MFMA path takes float16 activations, got {x.dtype}")
@@ -146,37 +194,37 @@ def tq1_gemm(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayou
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     need = handle.ternel_tq1_gemm_workspace_bytes(batch, layout.rows, layout.columns, config.k_split)
-    ws = torch.empty(max(need, 4), dtype=torch.uint8, device=x.device) if need else None
+    ws = workspace(x.device, need)
     _lib.check(handle.ternel_tq1_gemm(
-        blocks.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns,
-        _lib.DTYPE_F16, config.k_split, ws.data_ptr() if ws is not None else None, need,
-        _stream(x.device)))
+        packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns,
+        _lib.DTYPE_F16, config.k_split, ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0, _stream(x.device)))
     return out
 
 
-def tq1_linear(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+def tq1_linear(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
     """The library's own dispatch (``ternel_tq1_linear``) for a 2-D ``x``."""
-    check_blocks(blocks, layout=layout)
+    check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
     x = x.contiguous()
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     code = _DTYPE_CODE[x.dtype]
     need = handle.ternel_tq1_linear_workspace_bytes(batch, layout.rows, layout.columns, code)
-    ws = torch.empty(max(need, 4), dtype=torch.uint8, device=x.device) if need else None
+    ws = workspace(x.device, need)
     _lib.check(handle.ternel_tq1_linear(
-        blocks.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns, code,
-        ws.data_ptr() if ws is not None else None, need, _stream(x.device)))
+        packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns, code,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(x.device)))
     return out
 
 
-def tq1_get_rows(blocks: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
+def tq1_get_rows(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
                  dtype: torch.dtype) -> torch.Tensor:
     """Decode the rows named by ``indices`` (1-D); reference tq1_get_rows, kernels.py:1360-1398.
 
     Ids outside ``[0, rows)`` read as zeros, as the reference kernel does.
     """
-    check_blocks(blocks, layout=layout)
+    check_packed(packed, layout=layout)
     if dtype not in ACTIVATION_DTYPES:
         raise FormatError(f"output dtype must be one of {ACTIVATION_DTYPES}, got {dtype}")
     if indices.ndim != 1:
@@ -185,15 +233,24 @@ def tq1_get_rows(blocks: torch.Tensor, indices: torch.Tensor, *, layout: PackedT
         raise FormatError("indices are empty")
     if indices.dtype not in (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8):
         raise FormatError(f"indices must be an integer tensor, got {indices.dtype}")
-    ids = indices.to(device=blocks.device, dtype=torch.int64).contiguous()
-    out = torch.empty((ids.numel(), layout.columns), dtype=dtype, device=blocks.device)
+    ids = indices.to(device=packed.device, dtype=torch.int64).contiguous()
+    out = torch.empty((ids.numel(), layout.columns), dtype=dtype, device=packed.device)
     _lib.check(_lib.lib().ternel_tq1_get_rows(
-        blocks.data_ptr(), layout.rows, layout.columns, ids.data_ptr(), ids.numel(), out.data_ptr(),
-        _DTYPE_CODE[dtype], _stream(blocks.device)))
+        packed.data_ptr(), layout.rows, layout.columns, ids.data_ptr(), ids.numel(), out.data_ptr(),
+        _DTYPE_CODE[dtype], _stream(packed.device)))
     return out
 
 
-def lut23_grid(layout: PackedTensorLayout, batch: int, config: MatmulConfig) -> tuple[int, int, int]:
-    """Workgroups of a LUT23 launch: (row tiles, batch tiles, K split)."""
-    bt = config.batch_tile or (4 if batch >= 4 else 2 if batch >= 2 else 1)
-    return (math.ceil(layout.rows / LUT23_THREADS), math.ceil(batch / bt), max(config.k_split, 1))
+__all__ = [
+    "ACTIVATION_DTYPES",
+    "BLOCK_BYTES",
+    "GemmConfig",
+    "MatmulConfig",
+    "pack_weights",
+    "packed_shape",
+    "tq1_gemm",
+    "tq1_get_rows",
+    "tq1_linear",
+    "tq1_matmul",
+    "unpack_weights",
+]

@@ -4,10 +4,11 @@ Twins of the reference's module API (src/ternel_mlx/modules.py:425-549):
 ``packed_matmul``, ``PackedLinear`` and ``PackedEmbedding`` keep their names,
 constructor arguments, call signatures, output shapes/dtypes and FormatError
 messages. The only parameter a module owns is its packed weight -- here the
-canonical ``blocks`` buffer ``(rows, groups_per_row, 28)`` uint8, the exact
-bytes the gfx950 kernels stream -- and the reference's tiled ``codes``/``scales``
-pair is accepted on load (``load_packed``) and exposed as properties, both by
-exact byte permutation.
+``packed`` buffer: the canonical 28-byte blocks permuted into 64-row
+word-interleaved tiles, the exact words the gfx950 kernels stream. Canonical
+blocks (``load_blocks``) and the reference's tiled ``codes``/``scales`` pair
+(``load_packed``/``load_weights``) are accepted on load and exposed as
+properties, all by exact permutation.
 
 ``replace_with_packed`` is the torch counterpart of
 src/ternel_mlx/packed_model.py:72-92: it swaps every bias-free ``nn.Linear`` and
@@ -21,7 +22,16 @@ import torch
 from torch import nn
 
 from .format import BLOCK_BYTES, FormatError, as_device_blocks, validate_packed_codes
-from .kernels import GemmConfig, MatmulConfig, tq1_gemm, tq1_get_rows, tq1_matmul
+from .kernels import (
+    GemmConfig,
+    MatmulConfig,
+    pack_weights,
+    packed_shape,
+    tq1_gemm,
+    tq1_get_rows,
+    tq1_matmul,
+    unpack_weights,
+)
 from .layout import PackedTensorLayout, pack_blocks, unpack_blocks
 
 # Dispatch (src/ternel_mlx/modules.py:331-422, re-measured for MI355X): the
@@ -39,7 +49,7 @@ def select_kernel(layout: PackedTensorLayout, batch: int, dtype: torch.dtype) ->
     return "gemm"
 
 
-def packed_matmul(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+def packed_matmul(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
     """``x @ W.T`` for a packed ``W``, choosing the kernel by activation rows.
 
     Leading dimensions of ``x`` are kept (src/ternel_mlx/modules.py:425-457).
@@ -48,9 +58,9 @@ def packed_matmul(blocks: torch.Tensor, x: torch.Tensor, *, layout: PackedTensor
         raise FormatError(f"activation has {x.shape[-1]} columns, weight expects {layout.columns}")
     flat = x.reshape(-1, layout.columns)
     if select_kernel(layout, flat.shape[0], flat.dtype) == "gemm":
-        out = tq1_gemm(blocks, flat, layout=layout, config=GemmConfig())
+        out = tq1_gemm(packed, flat, layout=layout, config=GemmConfig())
     else:
-        out = tq1_matmul(blocks, flat, layout=layout, config=MatmulConfig())
+        out = tq1_matmul(packed, flat, layout=layout, config=MatmulConfig())
     return out.reshape(*x.shape[:-1], layout.rows)
 
 
@@ -62,10 +72,14 @@ class _PackedWeight(nn.Module):
         self.layout = layout
         if device is None and torch.cuda.is_available():
             device = torch.device("cuda", torch.cuda.current_device())
-        self.register_buffer("blocks", torch.zeros(layout.canonical_shape, dtype=torch.uint8, device=device))
+        self.register_buffer("packed", torch.zeros(packed_shape(layout), dtype=torch.int32, device=device))
 
     def load_blocks(self, blocks, *, validate: bool = True) -> None:
-        """Load canonical blocks (any shape holding ``rows * G`` 28-byte blocks)."""
+        """Load canonical blocks (any shape holding ``rows * G`` 28-byte blocks).
+
+        Every byte is scanned on the GPU first (fail-closed), then the blocks are
+        permuted into the packed layout.
+        """
         tensor = as_device_blocks(blocks)
         if tensor.shape[0] != self.layout.groups:
             raise FormatError(
@@ -74,7 +88,7 @@ class _PackedWeight(nn.Module):
             )
         if validate:
             validate_packed_codes(tensor)
-        self.blocks = tensor.reshape(self.layout.canonical_shape).to(self.blocks.device)
+        self.packed = pack_weights(tensor, layout=self.layout)
 
     def load_packed(self, codes, scales, *, validate: bool = True) -> None:
         """Load the reference's tiled ``codes`` (u8) / ``scales`` (<u2) arrays."""
@@ -98,8 +112,13 @@ class _PackedWeight(nn.Module):
         return self
 
     @property
+    def blocks(self) -> torch.Tensor:
+        """Canonical ``(rows, G, 28)`` blocks, by exact inverse permutation of ``packed``."""
+        return unpack_weights(self.packed, layout=self.layout)
+
+    @property
     def codes(self) -> np.ndarray:
-        """The reference's tiled code array, by exact permutation of ``blocks``."""
+        """The reference's tiled code array, by exact permutation of the blocks."""
         return pack_blocks(self.blocks.cpu().numpy(), layout=self.layout)[0]
 
     @property
@@ -123,7 +142,7 @@ class PackedLinear(_PackedWeight):
                 f"{self.layout.bits_per_weight:.3f} bits/weight")
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return packed_matmul(self.blocks, x, layout=self.layout)
+        return packed_matmul(self.packed, x, layout=self.layout)
 
 
 class PackedEmbedding(_PackedWeight):
@@ -144,12 +163,12 @@ class PackedEmbedding(_PackedWeight):
     def forward(self, indices: torch.Tensor) -> torch.Tensor:
         """Rows for ``indices`` of any shape; ids outside the table read as zeros."""
         flat = indices.reshape(-1)
-        rows = tq1_get_rows(self.blocks, flat, layout=self.layout, dtype=self.dtype)
+        rows = tq1_get_rows(self.packed, flat, layout=self.layout, dtype=self.dtype)
         return rows.reshape(*indices.shape, self.layout.columns)
 
     def as_linear(self, x: torch.Tensor) -> torch.Tensor:
         """Tied output head: the embedding table used as a matmul."""
-        return packed_matmul(self.blocks, x, layout=self.layout)
+        return packed_matmul(self.packed, x, layout=self.layout)
 
 
 def replace_with_packed(model: nn.Module, *, embedding_dtype: torch.dtype = torch.float16) -> nn.Module:

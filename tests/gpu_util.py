@@ -34,6 +34,14 @@ def layout(rows: int, columns: int) -> PackedTensorLayout:
     return PackedTensorLayout.for_tensor(rows, columns)
 
 
+def pack(blocks: np.ndarray) -> torch.Tensor:
+    """Canonical (rows, G, 28) host blocks -> packed device words."""
+    from ternel_amd.kernels import pack_weights
+
+    rows, g, _ = blocks.shape
+    return pack_weights(to_dev(blocks.reshape(-1, 28)), layout=layout(rows, g * 128))
+
+
 def positional_all_slots() -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """tests/test_mlx_kernels.py:107-135 construction: 243 rows x 25 groups; group g
     carries the byte under test in slot g; batch sample g has activation

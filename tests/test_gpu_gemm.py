@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import tq1_oracle as O
-from tests.gpu_util import layout, random_blocks, to_dev
+from tests.gpu_util import layout, pack, random_blocks, to_dev
 from ternel_amd.format import FormatError
 from ternel_amd.kernels import GemmConfig, tq1_gemm
 
@@ -26,7 +26,7 @@ FP16_UNIT_ROUNDOFF = 2.0 ** -11
 
 def run(blocks: np.ndarray, x16: np.ndarray, *, k_split: int = 0) -> np.ndarray:
     rows, g, _ = blocks.shape
-    out = tq1_gemm(to_dev(blocks), to_dev(x16), layout=layout(rows, g * 128), config=GemmConfig(k_split=k_split))
+    out = tq1_gemm(pack(blocks), to_dev(x16), layout=layout(rows, g * 128), config=GemmConfig(k_split=k_split))
     torch.cuda.synchronize()
     return out.float().cpu().numpy().astype(np.float64)
 
@@ -114,7 +114,7 @@ def test_gemm_propagates_non_finite_activations() -> None:
 
 
 def test_gemm_rejects_other_dtypes_and_bad_splits() -> None:
-    blocks = to_dev(random_blocks(256, 384, seed=1))
+    blocks = pack(random_blocks(256, 384, seed=1))
     lay = layout(256, 384)
     with pytest.raises(FormatError, match="float16"):
         tq1_gemm(blocks, torch.zeros((4, 384), device="cuda"), layout=lay)

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import tq1_oracle as O
-from tests.gpu_util import layout, positional_all_slots, positional_tail, random_blocks, to_dev
+from tests.gpu_util import layout, pack, positional_all_slots, positional_tail, random_blocks, to_dev
 from ternel_amd.format import FormatError
 from ternel_amd.kernels import MatmulConfig, tq1_matmul
 
@@ -27,7 +27,7 @@ def run(blocks: np.ndarray, x: np.ndarray, *, batch_tile: int = 1, k_split: int 
         dtype=torch.float32) -> np.ndarray:
     rows, g, _ = blocks.shape
     lay = layout(rows, g * 128)
-    out = tq1_matmul(to_dev(blocks), to_dev(x).to(dtype), layout=lay,
+    out = tq1_matmul(pack(blocks), to_dev(x).to(dtype), layout=lay,
                      config=MatmulConfig(batch_tile=batch_tile, k_split=k_split))
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
@@ -85,7 +85,7 @@ def test_activation_dtypes_round_once_at_the_store(dtype) -> None:
     raw = torch.from_numpy(rng.normal(0.0, 1.0, size=(3, 384)).astype(np.float32)).to(dtype)
     x = raw.float().numpy()
     lay = layout(256, 384)
-    out = tq1_matmul(to_dev(blocks), raw.to("cuda"), layout=lay, config=MatmulConfig(batch_tile=1, k_split=1))
+    out = tq1_matmul(pack(blocks), raw.to("cuda"), layout=lay, config=MatmulConfig(batch_tile=1, k_split=1))
     assert out.dtype == dtype
     want = O.lut23_matmul(blocks, x, rows=256, columns=384)
     # Only the final store is narrowed: the result is the fp32 answer rounded once.
@@ -163,7 +163,7 @@ def test_a_split_that_does_not_divide_the_groups_is_rejected() -> None:
 
 
 def test_activation_checks_match_the_reference_messages() -> None:
-    blocks = to_dev(random_blocks(256, 384, seed=1))
+    blocks = pack(random_blocks(256, 384, seed=1))
     lay = layout(256, 384)
     with pytest.raises(FormatError, match="activations have 256 columns, expected 384"):
         tq1_matmul(blocks, torch.zeros((1, 256), device="cuda"), layout=lay)
@@ -180,7 +180,7 @@ def test_auto_configuration_meets_the_north_star_tolerance(batch: int) -> None:
     rows, columns = 2048, 5120
     blocks = random_blocks(rows, columns, seed=batch)
     x = np.random.default_rng(batch).normal(0, 1, size=(batch, columns)).astype(np.float16)
-    got = tq1_matmul(to_dev(blocks), to_dev(x), layout=layout(rows, columns)).float().cpu().numpy()
+    got = tq1_matmul(pack(blocks), to_dev(x), layout=layout(rows, columns)).float().cpu().numpy()
     oracle = O.oracle_matmul(blocks, x.astype(np.float32), rows=rows, columns=columns)
     result = O.compare(got, oracle)
     assert result["normalised_max_abs_error"] < NORTH_STAR_TOLERANCE

@@ -9,7 +9,7 @@ import torch
 from torch import nn
 
 from oracle import tq1_oracle as O
-from tests.gpu_util import layout, random_blocks, to_dev
+from tests.gpu_util import layout, pack, random_blocks, to_dev
 from ternel_amd.format import FormatError
 from ternel_amd.kernels import tq1_get_rows
 from ternel_amd.layout import pack_blocks
@@ -24,7 +24,7 @@ def test_get_rows_is_bit_exact(rows: int, columns: int, dtype) -> None:
     blocks = random_blocks(rows, columns, seed=rows + 3)
     rng = np.random.default_rng(rows)
     ids = np.unique(np.concatenate([[0, rows - 1, rows // 2], rng.integers(0, rows, size=16)])).astype(np.int64)
-    got = tq1_get_rows(to_dev(blocks), to_dev(ids), layout=layout(rows, columns), dtype=dtype)
+    got = tq1_get_rows(pack(blocks), to_dev(ids), layout=layout(rows, columns), dtype=dtype)
     want = O.get_rows_reference(blocks, ids, rows=rows, columns=columns,
                                 dtype=np.float32 if dtype == torch.float32 else np.float16)
     np.testing.assert_array_equal(got.cpu().numpy(), want)
@@ -33,7 +33,7 @@ def test_get_rows_is_bit_exact(rows: int, columns: int, dtype) -> None:
 def test_get_rows_bf16_rounds_the_exact_value_once() -> None:
     blocks = random_blocks(300, 256, seed=9)
     ids = np.arange(0, 300, 7, dtype=np.int64)
-    got = tq1_get_rows(to_dev(blocks), to_dev(ids), layout=layout(300, 256), dtype=torch.bfloat16)
+    got = tq1_get_rows(pack(blocks), to_dev(ids), layout=layout(300, 256), dtype=torch.bfloat16)
     want = O.get_rows_reference(blocks, ids, rows=300, columns=256, dtype=np.float32)
     np.testing.assert_array_equal(got.float().cpu().numpy(), torch.from_numpy(want).to(torch.bfloat16).float().numpy())
 
@@ -41,7 +41,7 @@ def test_get_rows_bf16_rounds_the_exact_value_once() -> None:
 def test_get_rows_repeats_and_out_of_range_ids() -> None:
     blocks = random_blocks(512, 256, seed=44)
     ids = torch.tensor([7, 7, 511, 0, 7, 512, 100000, -1], dtype=torch.int64, device="cuda")
-    got = tq1_get_rows(to_dev(blocks), ids, layout=layout(512, 256), dtype=torch.float32).cpu().numpy()
+    got = tq1_get_rows(pack(blocks), ids, layout=layout(512, 256), dtype=torch.float32).cpu().numpy()
     np.testing.assert_array_equal(got[0], got[1])
     np.testing.assert_array_equal(got[0], got[4])
     assert not got[5:].any()
@@ -49,7 +49,7 @@ def test_get_rows_repeats_and_out_of_range_ids() -> None:
 
 
 def test_get_rows_rejects_bad_indices() -> None:
-    blocks = to_dev(random_blocks(256, 256, seed=1))
+    blocks = pack(random_blocks(256, 256, seed=1))
     with pytest.raises(FormatError, match="1-D"):
         tq1_get_rows(blocks, torch.zeros((2, 2), dtype=torch.int64, device="cuda"), layout=layout(256, 256),
                      dtype=torch.float32)
@@ -152,5 +152,5 @@ def test_replace_with_packed_swaps_every_linear_and_embedding() -> None:
 def test_packed_matmul_function_matches_the_module() -> None:
     module, blocks = loaded_linear(256, 384, seed=12)
     x = torch.randn(3, 384, device="cuda", dtype=torch.float16)
-    np.testing.assert_array_equal(packed_matmul(module.blocks, x, layout=module.layout).cpu().numpy(),
+    np.testing.assert_array_equal(packed_matmul(module.packed, x, layout=module.layout).cpu().numpy(),
                                   module(x).cpu().numpy())

@@ -196,10 +196,13 @@ def test_split_k_refusal_message() -> None:
 
 def test_workspace_queries() -> None:
     handle = _lib.lib()
+    counters = 64 * 1024  # fixed split-K counter region at the front of every workspace
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 1) == 0
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 8) == 8 * 256 * 4
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 8) == counters + 8 * 256 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, 1) == 0
-    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, 5) == 5 * 8 * 256 * 4
+    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, 5) == counters + 5 * 8 * 256 * 4
+    assert handle.ternel_tq1_packed_words(300, 640) == 5 * 5 * 7 * 64
+    assert handle.ternel_tq1_packed_words(300, 600) == 0
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path) -> None:
