@@ -304,40 +304,69 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
 // Illegal regular bytes index inside the group's 927 entries and the tail is
 // clamped, so no input reads outside the tables.
 // ---------------------------------------------------------------------------
+// Table tasks of one sub-chunk: 51 per (vector, group). A thread owns tasks
+// tid, tid + 256, ...; it loads their activations before anything else so the
+// in-order vmcnt wait of the build never waits behind the weight stream.
+constexpr int lut_task_count(int c, int bt) { return bt * c * kTasksPerGroup; }
+constexpr int lut_task_iters(int c, int bt) { return (lut_task_count(c, bt) + kThreads - 1) / kThreads; }
+
 template <typename T, int C, int BT>
-__device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats], const T *__restrict__ x,
-                                                 int64_t K, int M, int b0, int g0, int tid) {
-    for (int task = tid; task < BT * C * kTasksPerGroup; task += kThreads) {
+__device__ __forceinline__ void load_lut_inputs(T (&xv)[lut_task_iters(C, BT)][3], const T *__restrict__ x,
+                                                int64_t K, int M, int b0, int g0, int tid) {
+#pragma unroll
+    for (int it = 0; it < lut_task_iters(C, BT); ++it) {
+        // Clamped rather than skipped: every load issues unconditionally, which
+        // keeps the compiler's vmcnt accounting exact (no branch around loads).
+        const int task = min(tid + it * kThreads, lut_task_count(C, BT) - 1);
         const int j = task / (C * kTasksPerGroup);
         const int rem = task - j * (C * kTasksPerGroup);
         const int c = rem / kTasksPerGroup;
         const int k = rem - c * kTasksPerGroup;
         const int sample = min(b0 + j, M - 1);
         const T *xg = x + static_cast<int64_t>(sample) * K + static_cast<int64_t>(g0 + c) * kBlockWeights;
+        // L2 task k < 25: x[5k], x[5k+1]; L3 task: x[5s+2..5s+4]; tail: x[125..127].
+        // Kept raw: converting here would make the loads wait before the weight loads issue.
+        const int base = k < kFullSlots ? 5 * k : (k < 2 * kFullSlots ? 5 * (k - kFullSlots) + 2 : 125);
+        xv[it][0] = xg[base];
+        xv[it][1] = xg[base + 1];
+        xv[it][2] = xg[k < kFullSlots ? base + 1 : base + 2];
+    }
+}
+
+template <typename T, int C, int BT>
+__device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
+                                                 const T (&xv)[lut_task_iters(C, BT)][3], int tid) {
+#pragma unroll
+    for (int it = 0; it < lut_task_iters(C, BT); ++it) {
+        // A clamped (repeated) task writes the same values to the same entries.
+        const int task = min(tid + it * kThreads, lut_task_count(C, BT) - 1);
+        const int j = task / (C * kTasksPerGroup);
+        const int rem = task - j * (C * kTasksPerGroup);
+        const int c = rem / kTasksPerGroup;
+        const int k = rem - c * kTasksPerGroup;
         float *L = lut[j][c];
+        const float x0 = to_f32<T>(xv[it][0]);
+        const float x1 = to_f32<T>(xv[it][1]);
+        // (t - 1) * x as real products, so 0 * inf = NaN propagates as in the reference.
+        const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
+        const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
         if (k < kFullSlots) {
-            const float x0 = to_f32<T>(xg[5 * k]);
-            const float x1 = to_f32<T>(xg[5 * k + 1]);
-            const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
-            const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
             float *dst = L + k * kL2Entries;
 #pragma unroll
             for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
         } else {
+            const float x2 = to_f32<T>(xv[it][2]);
+            const float d[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
             const int s = k - kFullSlots;
-            const int base = s < kFullSlots ? 5 * s + 2 : 125;
-            const float x2 = to_f32<T>(xg[base]);
-            const float x3 = to_f32<T>(xg[base + 1]);
-            const float x4 = to_f32<T>(xg[base + 2]);
-            const float a[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
-            const float b[3] = {-1.0f * x3, 0.0f * x3, 1.0f * x3};
-            const float d[3] = {-1.0f * x4, 0.0f * x4, 1.0f * x4};
             float *dst = L + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
 #pragma unroll
             for (int e = 0; e < kL3Entries; ++e) dst[e] = (a[e % 3] + b[(e / 3) % 3]) + d[e / 9];
         }
     }
 }
+
+// s_waitcnt with vmcnt(0) and the other counters left alone (gfx9 encoding).
+__device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 template <typename T, int C, int BT>
 __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
@@ -356,16 +385,22 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
     const int g_begin = blockIdx.z * chunk_groups;
     const int g_end = g_begin + chunk_groups;
     const int64_t K = static_cast<int64_t>(G) * kBlockWeights;
-    const uint32_t *row_words = packed + static_cast<int64_t>(tile) * G * kTileGroupWords + lane;
+    // Waves past the last tile load (and discard) the last tile instead of
+    // branching around their loads.
+    const int load_tile = min(tile, (N + kTileRows - 1) / kTileRows - 1);
+    const uint32_t *row_words = packed + static_cast<int64_t>(load_tile) * G * kTileGroupWords + lane;
 
     float acc[BT];
 #pragma unroll
     for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
 
     for (int g0 = g_begin; g0 < g_end; g0 += C) {
-        // 1. This row's C blocks, in flight before the tables are built.
+        // 1. Activations for this thread's table tasks, then this row's C blocks:
+        //    the whole weight chunk is in flight while the tables are built.
+        T xv[lut_task_iters(C, BT)][3];
+        load_lut_inputs<T, C, BT>(xv, x, K, M, b0, g0, tid);
         uint32_t w[C][kBlockWords];
-        if (row_ok) {
+        {
             const uint32_t *p = row_words + static_cast<int64_t>(g0) * kTileGroupWords;
 #pragma unroll
             for (int c = 0; c < C; ++c)
@@ -375,11 +410,11 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
 
         // 2. Tables (after every lane is done reading the previous ones).
         if (g0 != g_begin) __syncthreads();
-        build_lut_tables<T, C, BT>(lut, x, K, M, b0, g0, tid);
+        build_lut_tables<T, C, BT>(lut, xv, tid);
         __syncthreads();
 
-        // 3. Consume.
-        if (row_ok) {
+        // 3. Consume (rows past N compute a discarded value).
+        {
 #pragma unroll
             for (int c = 0; c < C; ++c) {
                 const float scale = half_bits_to_float(w[c][0]);
@@ -414,30 +449,38 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
         }
         return;
     }
+    // Split: publish the partial with agent-coherent stores (they bypass the
+    // per-XCD L2, so no cache writeback is needed), wait until they are
+    // acknowledged, then count this chunk in. The workgroup that brings the
+    // count to k_split adds the chunks in chunk order with agent-coherent loads.
     if (row_ok) {
 #pragma unroll
         for (int j = 0; j < BT; ++j)
-            if (b0 + j < M) partial[(static_cast<int64_t>(blockIdx.z) * M + b0 + j) * N + row] = acc[j];
+            if (b0 + j < M)
+                __hip_atomic_store(partial + (static_cast<int64_t>(blockIdx.z) * M + b0 + j) * N + row, acc[j],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __threadfence();
+    wait_vector_memory();
     __syncthreads();
     unsigned *counter = counters + static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
-    if (tid == 0) s_last = atomicAdd(counter, 1u) == static_cast<unsigned>(k_split - 1);
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 static_cast<unsigned>(k_split - 1);
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     if (row_ok) {
+        const int64_t stride = static_cast<int64_t>(M) * N;
 #pragma unroll
         for (int j = 0; j < BT; ++j) {
             if (b0 + j >= M) continue;
             const float *src = partial + static_cast<int64_t>(b0 + j) * N + row;
-            const int64_t stride = static_cast<int64_t>(M) * N;
-            float a = __builtin_nontemporal_load(src);
-            for (int z = 1; z < k_split; ++z) a += __builtin_nontemporal_load(src + z * stride);
+            float a = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int z = 1; z < k_split; ++z)
+                a += __hip_atomic_load(src + z * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(a);
         }
     }
-    if (tid == 0) atomicExch(counter, 0u);
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <typename T>
