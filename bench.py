@@ -48,6 +48,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-model-stream", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
 
@@ -120,14 +121,38 @@ def main() -> int:
     import torch
 
     from ternel_amd import synthetic
-    from ternel_amd.kernels import GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_matmul
+    from ternel_amd.kernels import GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_get_rows, tq1_matmul
     from ternel_amd.layout import PackedTensorLayout
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    stream = torch.cuda.current_stream(dev)
 
-    # ---- config 1: ring of distinct weight copies --------------------------------
+    def events() -> tuple:
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def graph_of(fn):
+        """Capture fn() into a HIP graph (after one eager call that sizes the workspace)."""
+        fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        torch.cuda.synchronize()
+        return graph
+
+    def time_graph(graph, replays: int = 1) -> float:
+        """ms per replay, events around the replays on the current stream."""
+        stream = torch.cuda.current_stream(dev)
+        a, b = events()
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / replays
+
+    # ---- config 1: ring of distinct weight copies, cold ----------------------------
     step_bytes = sum(packed_bytes(K, N) for _, K, N in C1_SHAPES)
     ring = max(2, -(-RING_BYTES_MIN // step_bytes))
     layouts = [PackedTensorLayout.for_tensor(N, K) for _, K, N in C1_SHAPES]
@@ -136,49 +161,52 @@ def main() -> int:
     xs = [synthetic.device_activations(1, K, seed=synthetic.SEED_BASE + 1 + i) for i, (_, K, _) in enumerate(C1_SHAPES)]
     config = MatmulConfig()
 
-    def step(r: int, starts=None, ends=None) -> None:
+    def step(r: int) -> None:
         for i, lay in enumerate(layouts):
-            if starts is not None:
-                starts[i].record(stream)
             tq1_matmul(weights[r][i], xs[i], layout=lay, config=config)
-            if ends is not None:
-                ends[i].record(stream)
 
     for w in range(args.warmup):
         step(w % ring)
     torch.cuda.synchronize()
 
-    starts = [[torch.cuda.Event(enable_timing=True) for _ in C1_SHAPES] for _ in range(args.steps)]
-    ends = [[torch.cuda.Event(enable_timing=True) for _ in C1_SHAPES] for _ in range(args.steps)]
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for s in range(args.steps):
-        step(s % ring, starts[s], ends[s])
-    t1.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
-    ms_per_step = total_ms / args.steps
-    per_kernel_ms = [sum(starts[s][i].elapsed_time(ends[s][i]) for s in range(args.steps)) / args.steps
-                     for i in range(len(C1_SHAPES))]
+    # Timed region: exactly `steps` steps, replayed from one graph (no host
+    # launch overhead between kernels), synchronize on both sides.
+    steps_graph = graph_of(lambda: [step(s % ring) for s in range(args.steps)])
+    ms_per_step = time_graph(steps_graph) / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del steps_graph
 
-    dominant = 0  # gate/up: the largest packed matrix, first in the step
-    dom_bytes = packed_bytes(C1_SHAPES[dominant][1], C1_SHAPES[dominant][2])
-    achieved = dom_bytes / (per_kernel_ms[dominant] * 1e-3) / 1e9
-
-    # Warm (weights resident in MALL/L2) for context.
-    warm_iters = 100
-    w0 = torch.cuda.Event(enable_timing=True)
-    w1 = torch.cuda.Event(enable_timing=True)
-    tq1_matmul(weights[0][0], xs[0], layout=layouts[0], config=config)
-    w0.record(stream)
-    for _ in range(warm_iters):
-        tq1_matmul(weights[0][0], xs[0], layout=layouts[0], config=config)
-    w1.record(stream)
+    # Dominant kernel (gate/up): per-launch HIP event pairs on the launch stream.
+    dominant = 0
+    dom_name, dom_K, dom_N = C1_SHAPES[dominant]
+    dom_bytes = packed_bytes(dom_K, dom_N)
+    stream = torch.cuda.current_stream(dev)
+    pairs = [events() for _ in range(args.steps)]
+    for s in range(args.steps):
+        pairs[s][0].record(stream)
+        tq1_matmul(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant], config=config)
+        pairs[s][1].record(stream)
     torch.cuda.synchronize()
-    warm_ms = w0.elapsed_time(w1) / warm_iters
+    launch_ms = sorted(a.elapsed_time(b) for a, b in pairs)
+    mean_launch_ms = sum(launch_ms) / len(launch_ms)
+    median_launch_ms = launch_ms[len(launch_ms) // 2]
+    achieved = dom_bytes / (mean_launch_ms * 1e-3) / 1e9
+    # Same kernel back to back inside a graph: launch + gap, for comparison.
+    dom_graph = graph_of(lambda: [tq1_matmul(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant],
+                                             config=config) for s in range(args.steps)])
+    graph_launch_ms = time_graph(dom_graph) / args.steps
+    del dom_graph
+    per_matrix = {}
+    for i, (name, K, N) in enumerate(C1_SHAPES):
+        g = graph_of(lambda i=i: [tq1_matmul(weights[s % ring][i], xs[i], layout=layouts[i], config=config)
+                                  for s in range(ring * 4)])
+        ms = time_graph(g) / (ring * 4)
+        per_matrix[name] = {"graph_ms_per_launch": round(ms, 5), "GB/s": round(packed_bytes(K, N) / (ms * 1e-3) / 1e9, 1)}
+        del g
+    warm = graph_of(lambda: [tq1_matmul(weights[0][dominant], xs[dominant], layout=layouts[dominant], config=config)
+                             for _ in range(100)])
+    warm_ms = time_graph(warm) / 100
+    del warm
 
     result = {
         "metric": "packed-weight GB/s at M=1 (TQ1_G128 decode GEMV, 27B-class shapes)",
@@ -194,7 +222,7 @@ def main() -> int:
         "dtype": "f32",
         "activation_dtype": "f16",
         "data": "synthetic (BASELINE trit/scale/activation distributions; cold ring of "
-                f"{ring} distinct weight copies, {ring * step_bytes / 2**20:.0f} MiB)",
+                f"{ring} distinct weight copies, {ring * step_bytes / 2**20:.0f} MiB); steps replayed from a HIP graph",
         "config": {
             "workload": "BASELINE configs[1]: M=1 GEMV over gate/up 5120->17408, down 17408->5120, "
                         "QKV 5120->8192 (one step = the three GEMVs)",
@@ -202,8 +230,7 @@ def main() -> int:
             "packed_bytes_per_step": step_bytes,
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         },
-        "per_matrix": {name: {"ms": round(ms, 5), "GB/s": round(packed_bytes(K, N) / (ms * 1e-3) / 1e9, 1)}
-                       for (name, K, N), ms in zip(C1_SHAPES, per_kernel_ms)},
+        "per_matrix": per_matrix,
         "warm_gate_up_GBs": round(dom_bytes / (warm_ms * 1e-3) / 1e9, 1),
         "roofline": {
             "bound": "hbm",
@@ -212,40 +239,82 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "gate/up GEMV 5120->17408 (lut_gemv_kernel, fused ordered split-K)",
+            "kernel": f"{dom_name} GEMV K={dom_K} N={dom_N} (lut_gemv_kernel, fused ordered split-K)",
             "bytes_per_launch": dom_bytes,
+            "mean_launch_us": round(mean_launch_ms * 1e3, 3),
+            "median_launch_us": round(median_launch_ms * 1e3, 3),
+            "graph_back_to_back_us": round(graph_launch_ms * 1e3, 3),
         },
     }
+    del weights
 
-    # ---- config 3: prefill GEMM M=512 ------------------------------------------
+    # ---- config 3: prefill GEMM M=512 -------------------------------------------
     if not args.no_prefill:
         prefill = {}
         for name, K, N in C3_SHAPES:
             lay = PackedTensorLayout.for_tensor(N, K)
             blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
             xp = synthetic.device_activations(512, K, seed=synthetic.SEED_BASE + 3, sigma=0.5)
-            for _ in range(3):
-                tq1_gemm(blk, xp, layout=lay, config=GemmConfig())
-            p0 = torch.cuda.Event(enable_timing=True)
-            p1 = torch.cuda.Event(enable_timing=True)
-            iters = 20
-            p0.record(stream)
-            for _ in range(iters):
-                tq1_gemm(blk, xp, layout=lay, config=GemmConfig())
-            p1.record(stream)
-            torch.cuda.synchronize()
-            ms = p0.elapsed_time(p1) / iters
+            g = graph_of(lambda: [tq1_gemm(blk, xp, layout=lay, config=GemmConfig()) for _ in range(20)])
+            ms = time_graph(g) / 20
             tflops = 2 * 512 * K * N / (ms * 1e-3) / 1e12
             prefill[name] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2),
                              "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
-            del blk, xp
+            del g, blk, xp
         result["prefill_m512"] = prefill
+
+    # ---- config 4: 64-layer weight stream + one embedding row -------------------
+    if not args.no_model_stream:
+        result["model_stream"] = model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows,
+                                              PackedTensorLayout, MatmulConfig, graph_of, time_graph)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+C4_LAYER = (("qkv", 5120, 8192), ("o", 8192, 5120), ("gate_up", 5120, 34816), ("down", 17408, 5120))
+C4_LAYERS = 64
+C4_VOCAB = 151936
+
+
+def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, PackedTensorLayout, MatmulConfig,
+                 graph_of, time_graph) -> dict:
+    """64 sequential layers of M=1 GEMVs (4.92 GB of packed weights,
+    larger than every cache, so each token reads them cold), then one embedding row."""
+    layouts = [PackedTensorLayout.for_tensor(N, K) for _, K, N in C4_LAYER]
+    weights = [[pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 4 + 10 * layer + i), layout=lay)
+                for i, ((_, K, N), lay) in enumerate(zip(C4_LAYER, layouts))] for layer in range(C4_LAYERS)]
+    xs = {K: synthetic.device_activations(1, K, seed=synthetic.SEED_BASE + 4 + K) for _, K, _ in C4_LAYER}
+    table_layout = PackedTensorLayout.for_tensor(C4_VOCAB, 5120)
+    table = pack_weights(synthetic.device_blocks(C4_VOCAB, 5120, seed=synthetic.SEED_BASE + 44), layout=table_layout)
+    token = torch.tensor([75967], dtype=torch.int64, device="cuda")
+    config = MatmulConfig()
+
+    def token_pass() -> None:
+        for layer in range(C4_LAYERS):
+            for i, (_, K, _) in enumerate(C4_LAYER):
+                tq1_matmul(weights[layer][i], xs[K], layout=layouts[i], config=config)
+        tq1_get_rows(table, token, layout=table_layout, dtype=torch.float16)
+
+    graph = graph_of(token_pass)
+    replays = 5
+    ms = time_graph(graph, replays)
+    total = C4_LAYERS * sum(packed_bytes(K, N) for _, K, N in C4_LAYER)
+    gather = graph_of(lambda: [tq1_get_rows(table, token, layout=table_layout, dtype=torch.float16) for _ in range(100)])
+    gather_us = time_graph(gather) / 100 * 1e3
+    del graph, gather, weights, table
+    return {
+        "workload": "BASELINE configs[4]: 64 x (QKV 5120->8192, O 8192->5120, gate+up 5120->34816, "
+                    "down 17408->5120) M=1 GEMVs + 1 embedding row of 151936x5120, one HIP graph per token",
+        "packed_bytes": total,
+        "ms_per_token": round(ms, 4),
+        "GB/s": round(total / (ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "embedding_row_us_graph": round(gather_us, 3),
+    }
 
 
 if __name__ == "__main__":

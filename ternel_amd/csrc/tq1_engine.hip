@@ -365,6 +365,23 @@ __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
     }
 }
 
+// Adds partial[0..k) (stride apart) left to right. The agent-coherent loads are
+// issued eight at a time, so a long split costs a few round trips, not k.
+__device__ __forceinline__ float sum_partials_in_order(const float *src, int64_t stride, int k) {
+    float a = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int z = 1;
+    for (; z + 8 <= k; z += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            v[u] = __hip_atomic_load(src + (z + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a += v[u];
+    }
+    for (; z < k; ++z) a += __hip_atomic_load(src + z * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return a;
+}
+
 // s_waitcnt with vmcnt(0) and the other counters left alone (gfx9 encoding).
 __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
@@ -474,10 +491,7 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
         for (int j = 0; j < BT; ++j) {
             if (b0 + j >= M) continue;
             const float *src = partial + static_cast<int64_t>(b0 + j) * N + row;
-            float a = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (int z = 1; z < k_split; ++z)
-                a += __hip_atomic_load(src + z * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(a);
+            y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(sum_partials_in_order(src, stride, k_split));
         }
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -11,7 +11,7 @@ Outputs are fresh tensors in the activation dtype.
 
 Split-K workspaces: the LUT23 kernel reduces its K chunks inside the launch
 through arrival counters that must start at zero and are left at zero, so the
-workspace is allocated zero-filled once per (device, stream) and reused.
+workspace is allocated zero-filled once per device and reused.
 """
 
 from __future__ import annotations
@@ -132,21 +132,26 @@ def check_activations(x: torch.Tensor, *, layout: PackedTensorLayout) -> int:
     return x.shape[0]
 
 
-_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+_WORKSPACES: dict[int, torch.Tensor] = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Zero-initialised scratch for split-K, one per (device, stream), grown on demand.
+    """Zero-initialised split-K scratch, one per device, grown on demand.
 
     The LUT23 kernel leaves its arrival counters at zero after every launch, so
-    the buffer only needs zeroing when it is created.
+    the buffer only needs zeroing when it is created -- which never happens
+    inside a graph capture once an eager call of the same size has run. Calls
+    sharing the buffer must not run concurrently (one stream per device).
     """
     if nbytes == 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), _stream(device))
+    key = device.index if device.index is not None else torch.cuda.current_device()
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("split-K workspace must be sized by an eager call before graph capture")
+        buf = torch.zeros(max(nbytes, 1 << 22), dtype=torch.uint8, device=device)
+        torch.cuda.synchronize(device)
         _WORKSPACES[key] = buf
     return buf
 
