@@ -365,20 +365,50 @@ __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
     }
 }
 
-// Adds partial[0..k) (stride apart) left to right. The agent-coherent loads are
-// issued eight at a time, so a long split costs a few round trips, not k.
+// LUT23 split of the 25 code bytes of a block, two bytes per 16-bit-packed
+// operation: hi = (p * 57) >> 9 == p / 9 (exact for p <= 511), lo = p - 9 hi.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void split_pair(uint32_t pair, uint32_t &lo_a, uint32_t &hi_a, uint32_t &lo_b,
+                                           uint32_t &hi_b) {
+    u16x2 p = __builtin_bit_cast(u16x2, pair);
+    const u16x2 h = (p * static_cast<unsigned short>(57)) >> static_cast<unsigned short>(9);
+    const u16x2 l = p - h * static_cast<unsigned short>(9);
+    lo_a = l.x;
+    hi_a = h.x;
+    lo_b = l.y;
+    hi_b = h.y;
+}
+
+// All four bytes of a block word: lo/hi for byte b of the word.
+__device__ __forceinline__ void split_word(uint32_t word, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+    split_pair(word & 0x00ff00ffu, lo[0], hi[0], lo[2], hi[2]);         // bytes 0 and 2
+    split_pair((word >> 8) & 0x00ff00ffu, lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
+}
+
+// Adds partial[0..k) (stride apart) left to right. The agent-coherent loads of
+// up to 32 chunks are all issued before the first add, so a split costs one
+// memory round trip here rather than one per chunk.
 __device__ __forceinline__ float sum_partials_in_order(const float *src, int64_t stride, int k) {
-    float a = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int z = 1;
-    for (; z + 8 <= k; z += 8) {
-        float v[8];
+    constexpr int kBatch = 32;
+    float a = 0.0f;
+    for (int z0 = 0; z0 < k; z0 += kBatch) {
+        float v[kBatch];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            v[u] = __hip_atomic_load(src + (z + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int u = 0; u < kBatch; ++u)
+            v[u] = z0 + u < k ? __hip_atomic_load(src + (z0 + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : 0.0f;
+        if (z0 == 0) {
+            a = v[0];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) a += v[u];
+            for (int u = 1; u < kBatch; ++u)
+                if (u < k) a += v[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (z0 + u < k) a += v[u];
+        }
     }
-    for (; z < k; ++z) a += __hip_atomic_load(src + z * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return a;
 }
 
@@ -430,28 +460,40 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
         build_lut_tables<T, C, BT>(lut, xv, tid);
         __syncthreads();
 
-        // 3. Consume (rows past N compute a discarded value).
+        // 3. Consume (rows past N compute a discarded value). The C blocks are
+        //    walked word by word together, giving C independent add chains to
+        //    hide LDS latency; within a block the order is slot 0..24, tail,
+        //    then one fma with the scale, and blocks fold into acc in order.
         {
+            float sum[C][BT];
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int j = 0; j < BT; ++j) sum[c][j] = 0.0f;
+#pragma unroll
+            for (int word = 0; word < kBlockWords; ++word) {
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    uint32_t lo[4], hi[4];
+                    split_word(w[c][word], lo, hi);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
+                        if (s < 0 || s >= kFullSlots) continue;
+#pragma unroll
+                        for (int j = 0; j < BT; ++j)
+                            sum[c][j] += lut[j][c][s * kL2Entries + lo[b]] + lut[j][c][kL3Base + s * kL3Entries + hi[b]];
+                    }
+                }
+            }
 #pragma unroll
             for (int c = 0; c < C; ++c) {
                 const float scale = half_bits_to_float(w[c][0]);
-                float sum[BT];
-#pragma unroll
-                for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
-#pragma unroll
-                for (int s = 0; s < kFullSlots; ++s) {
-                    const uint32_t p = block_byte(w[c], 2 + s);
-                    const uint32_t hi = (p * 57u) >> 9;
-                    const uint32_t lo = p - 9u * hi;
-#pragma unroll
-                    for (int j = 0; j < BT; ++j)
-                        sum[j] += lut[j][c][s * kL2Entries + lo] + lut[j][c][kL3Base + s * kL3Entries + hi];
-                }
                 const uint32_t tail = min(w[c][6] >> 24, kMaxTailByte);
 #pragma unroll
                 for (int j = 0; j < BT; ++j) {
-                    sum[j] += lut[j][c][kTailBase + tail];
-                    acc[j] = fmaf(scale, sum[j], acc[j]);
+                    sum[c][j] += lut[j][c][kTailBase + tail];
+                    acc[j] = fmaf(scale, sum[c][j], acc[j]);
                 }
             }
         }
