@@ -568,18 +568,44 @@ constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
 constexpr int kGemmStride = kBlockWeights + 8;  // halves per LDS row
 
+// Decodes weights k = 64H .. 64H+63 of one block into 32 dwords = 64 fp16
+// (t - 1) * scale values in k order. Digits come from a mul-shift chain
+// (q / 3 == (q * 171) >> 9 for q < 256); each pair of adjacent weights is one
+// v_perm_b32 byte select from the 8-byte table {-s, z, +s}, selector
+// d * 0x202 + 0x100 per half. z is 0, or NaN when the scale is inf/NaN, so
+// that (t - 1) * s keeps IEEE semantics (0 * inf = NaN) exactly.
 template <int H>
-__device__ __forceinline__ void decode_half_block(const uint32_t (&w)[kBlockWords], float scale,
-                                                  _Float16 (&out)[64]) {
+__device__ __forceinline__ void decode_half_block(const uint32_t (&w)[kBlockWords], uint32_t (&out)[32]) {
+    const uint32_t s = w[0] & 0xffffu;
+    const uint32_t zero = (s & 0x7c00u) == 0x7c00u ? 0x7e00u : 0u;
+    const uint32_t table_lo = (zero << 16) | (s ^ 0x8000u);  // bytes 0-1: -s, bytes 2-3: z
+    const uint32_t table_hi = s;                             // bytes 4-5: +s
+    // Slots touched by this half: [first_slot, last_slot].
+    constexpr int first_slot = H == 0 ? 0 : 12;
+    constexpr int last_slot = H == 0 ? 12 : kFullSlots;  // slot 25 is the tail byte
+    uint32_t digit[(last_slot - first_slot + 1) * 5];
 #pragma unroll
-    for (int kk = 0; kk < 64; ++kk) {
-        const int k = H * 64 + kk;
-        const int s = k < 125 ? k / 5 : kFullSlots;
-        const int d = k < 125 ? k % 5 : k - 125;
-        const uint32_t b = block_byte(w, 2 + s);
-        const uint32_t p3 = d == 0 ? 1u : d == 1 ? 3u : d == 2 ? 9u : d == 3 ? 27u : 81u;
-        const uint32_t t = (b / p3) % 3u;
-        out[kk] = static_cast<_Float16>((static_cast<float>(t) - 1.0f) * scale);
+    for (int sl = first_slot; sl <= last_slot; ++sl) {
+        uint32_t q = block_byte(w, 2 + sl);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const uint32_t q3 = (q * 171u) >> 9;
+            digit[(sl - first_slot) * 5 + i] = q - 3u * q3;
+            q = q3;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 32; ++p) {
+        uint32_t d2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int k = H * 64 + 2 * p + e;
+            const int sl = k < 125 ? k / 5 : kFullSlots;
+            const int i = k < 125 ? k % 5 : k - 125;
+            d2[e] = digit[(sl - first_slot) * 5 + i];
+        }
+        const uint32_t pair = d2[0] | (d2[1] << 16);  // < 2^24: digits are 0..2 for legal bytes, < 4 always
+        out[p] = __builtin_amdgcn_perm(table_hi, table_lo, __umul24(pair, 0x0202u) + 0x01000100u);
     }
 }
 
@@ -609,56 +635,60 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Decoder assignment: lanes own consecutive rows (coalesced word loads).
+    // Decoder assignment: lanes own consecutive rows (coalesced word loads);
+    // rows past N decode the last row and their tile rows are never stored.
     const int dec_row = tid & (kGemmBN - 1);
     const int dec_half = tid / kGemmBN;
-    const int dec_n = n0 + dec_row;
+    const int dec_n = min(n0 + dec_row, N - 1);
+    const uint32_t *dec_words =
+        packed + static_cast<int64_t>(dec_n / kTileRows) * G * kTileGroupWords + (dec_n % kTileRows);
+    // Activation assignment: 128 rows x 16 chunks of 8 halves, 8 per thread;
+    // rows past M read row M-1 and are never stored.
+    const _Float16 *x_rows[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int idx = tid + i * kThreads;
+        x_rows[i] = x + static_cast<int64_t>(min(m0 + (idx >> 4), M - 1)) * K + (idx & 15) * 8;
+    }
+
+    // Prefetch the first group.
+    half8 xv[8];
+    uint32_t wv[kBlockWords];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        xv[i] = *reinterpret_cast<const half8 *>(x_rows[i] + static_cast<int64_t>(g_begin) * kBlockWeights);
+#pragma unroll
+    for (int j = 0; j < kBlockWords; ++j) wv[j] = dec_words[static_cast<int64_t>(g_begin) * kTileGroupWords + j * kTileRows];
 
     for (int g = g_begin; g < g_end; ++g) {
-        // Activation tile: 128 rows x 16 chunks of 8 halves.
+        // Stage this group: activations as loaded, weights decoded.
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int idx = tid + i * kThreads;
-            const int r = idx >> 4;
-            const int c8 = idx & 15;
-            const int m = m0 + r;
-            half8 v;
-            if (m < M) {
-                v = *reinterpret_cast<const half8 *>(x + static_cast<int64_t>(m) * K +
-                                                     static_cast<int64_t>(g) * kBlockWeights + c8 * 8);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = static_cast<_Float16>(0.0f);
-            }
-            *reinterpret_cast<half8 *>(xs + r * kGemmStride + c8 * 8) = v;
+            *reinterpret_cast<half8 *>(xs + (idx >> 4) * kGemmStride + (idx & 15) * 8) = xv[i];
         }
-        // Weight tile: each thread decodes half a block of one row.
         {
-            _Float16 wv[64];
-            if (dec_n < N) {
-                uint32_t w[kBlockWords];
-                const uint32_t *p = packed + (static_cast<int64_t>(dec_n / kTileRows) * G + g) * kTileGroupWords +
-                                    (dec_n % kTileRows);
-#pragma unroll
-                for (int j = 0; j < kBlockWords; ++j) w[j] = p[j * kTileRows];
-                const float scale = half_bits_to_float(w[0]);
-                if (dec_half == 0)
-                    decode_half_block<0>(w, scale, wv);
-                else
-                    decode_half_block<1>(w, scale, wv);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 64; ++e) wv[e] = static_cast<_Float16>(0.0f);
-            }
+            uint32_t dec[32];
+            if (dec_half == 0)
+                decode_half_block<0>(wv, dec);
+            else
+                decode_half_block<1>(wv, dec);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                half8 v;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = wv[q * 8 + e];
-                *reinterpret_cast<half8 *>(ws + dec_row * kGemmStride + dec_half * 64 + q * 8) = v;
+                uint4 v = {dec[4 * q], dec[4 * q + 1], dec[4 * q + 2], dec[4 * q + 3]};
+                *reinterpret_cast<uint4 *>(ws + dec_row * kGemmStride + dec_half * 64 + q * 8) = v;
             }
         }
         __syncthreads();
+        // Next group's operands are in flight during this group's MFMAs.
+        if (g + 1 < g_end) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                xv[i] = *reinterpret_cast<const half8 *>(x_rows[i] + static_cast<int64_t>(g + 1) * kBlockWeights);
+#pragma unroll
+            for (int j = 0; j < kBlockWords; ++j)
+                wv[j] = dec_words[static_cast<int64_t>(g + 1) * kTileGroupWords + j * kTileRows];
+        }
 #pragma unroll
         for (int kk = 0; kk < kBlockWeights / 16; ++kk) {
             half8 a[2], b[2];
@@ -724,8 +754,9 @@ int check_geometry(int64_t M, int64_t rows, int64_t columns) {
     return TERNEL_TQ1_OK;
 }
 
-// Workgroups a K split is sized to reach: a few resident per CU on the 256-CU part.
-constexpr int64_t kLutTargetWorkgroups = 512;
+// Above this many K chunks the split-K fix-up costs more than the extra
+// workgroups buy (measured, see plan_lut).
+constexpr int64_t kLutMaxChunks = 20;
 
 // The split-K workspace starts with a fixed region of arrival counters, one per
 // (row block, batch tile), that is all-zero between calls. Fixing its size keeps
@@ -776,15 +807,19 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
         plan->chunk = c;
         plan->k_split = k_split;
     } else {
-        // Largest compiled chunk that still offers the target number of workgroups.
+        // Measured on MI355X over the 27B shapes (graph-replayed, cold): four
+        // groups per workgroup wins (gate/up 10.6 us at k=10 vs 13.1 at k=5 and
+        // 13.1 at k=20; QKV, O and the 4096 square likewise), except where that
+        // leaves more than kLutMaxChunks K chunks to fix up -- down (G=136) runs
+        // 13.3 us at k=17 against 15.3 at k=34 -- where eight groups do.
         int c = 1;
-        for (int cand : {8, 4, 2}) {
-            if (!lut_chunk_supported(batch_tile, cand) || G % cand) continue;
-            if (plan->row_blocks * plan->batch_tiles * (G / cand) >= kLutTargetWorkgroups) {
+        for (int cand : {4, 2}) {
+            if (lut_chunk_supported(batch_tile, cand) && G % cand == 0) {
                 c = cand;
                 break;
             }
         }
+        if (G / c > kLutMaxChunks && G % 8 == 0 && lut_chunk_supported(batch_tile, 8)) c = 8;
         plan->chunk = c;
         plan->chunk_groups = c;
         plan->k_split = static_cast<int>(G / c);
