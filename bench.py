@@ -11,10 +11,13 @@ Inputs are resident in HBM before the timed region starts.
 ``value`` = packed weight bytes per step / wall time per step (events around
 the whole timed region, launch gaps included). ``roofline`` is for the dominant
 kernel (the gate/up GEMV): packed bytes per launch / its average launch
-duration, from per-launch HIP event pairs recorded on the launch stream inside
-the same timed region. The M=512 prefill GEMM is reported as a
-secondary figure in TFLOP/s against the fp16 MFMA peak, and the reference's
-CPU decode+matmul path (the oracle restatement) is timed on the host cores on a
+duration, from HIP events on the launch stream around `steps` cold launches
+replayed back to back from one graph; ``traffic`` is the HBM bytes per launch
+from the calibrated rocprofv3 --pmc passes recorded under profiles/. Secondary
+figures: the small-batch GEMM (configs[2], M=2..64, GB/s), the prefill GEMM
+(configs[3], M=512 and 2048, TFLOP/s against the fp16 MFMA peak), the 64-layer
+weight stream with one embedding row, and the reference's CPU
+decode+matmul path (the oracle restatement) timed on the host cores on a
 bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -34,6 +37,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 
 C1_SHAPES = (("gate_up", 5120, 17408), ("down", 17408, 5120), ("qkv", 5120, 8192))  # (name, K, N)
 C3_SHAPES = (("gate_up", 5120, 17408), ("down", 17408, 5120))
+SMALL_BATCHES = (2, 4, 8, 16, 32, 64)
+PREFILL_BATCHES = (512, 2048)
 RING_BYTES_MIN = 600 * 1024 * 1024  # > 2 x (256 MiB MALL + L2)
 
 
@@ -49,7 +54,13 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-model-stream", action="store_true")
+    p.add_argument("--no-small-batch", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="only launch the dominant kernel eagerly over the cold ring, then a plain copy of "
+                        "COPY_BYTES, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    p.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                   help="summarise a rocprofv3 kernel_trace.csv per (kernel, grid) and exit")
     return p.parse_args()
 
 
@@ -110,8 +121,47 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def trace_summary(path: str) -> int:
+    """Per-(kernel, grid) launch statistics from a rocprofv3 kernel_trace.csv: the
+    kernel statistics file groups every grid of one template instance together."""
+    import csv
+    import statistics
+
+    groups: dict = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            key = (row["Kernel_Name"], row["Grid_Size_X"], row["Grid_Size_Y"], row["Grid_Size_Z"])
+            groups.setdefault(key, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    print(f"{'calls':>6} {'avg_us':>9} {'median_us':>9} {'min_us':>8} {'max_us':>8}  grid (x,y,z)  kernel")
+    for (name, gx, gy, gz), ns in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print(f"{len(ns):6d} {statistics.fmean(ns) / 1e3:9.3f} {statistics.median(ns) / 1e3:9.3f} "
+              f"{min(ns) / 1e3:8.3f} {max(ns) / 1e3:8.3f}  ({gx},{gy},{gz})  {name[:110]}")
+    return 0
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gate_up_gemv_traffic.md")
+
+
+def measured_traffic() -> dict | None:
+    """HBM bytes per launch of the dominant kernel, from the two calibrated
+    rocprofv3 --pmc passes recorded in the profile (a fenced json block)."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    if "```json" not in text:
+        return None
+    block = text.split("```json", 1)[1].split("```", 1)[0]
+    return json.loads(block)
+
+
+COPY_BYTES = 256 * 1024 * 1024
+
+
 def main() -> int:
     args = parse()
+    if args.trace_summary:
+        return trace_summary(args.trace_summary)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the TQ1 path runs on a single MI355X in this build "
@@ -121,8 +171,10 @@ def main() -> int:
     import torch
 
     from ternel_amd import synthetic
-    from ternel_amd.kernels import GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_get_rows, tq1_matmul
+    from ternel_amd.kernels import (GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_get_rows, tq1_linear,
+                                    tq1_matmul)
     from ternel_amd.layout import PackedTensorLayout
+    from ternel_amd.modules import select_kernel
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -169,6 +221,21 @@ def main() -> int:
         step(w % ring)
     torch.cuda.synchronize()
 
+    if args.traffic_probe:
+        # Eager launches only (counter collection serialises dispatches): the dominant
+        # kernel over the cold ring, then a plain copy of known size for calibration.
+        for s in range(args.steps):
+            tq1_matmul(weights[s % ring][0], xs[0], layout=layouts[0], config=config)
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_probe": C1_SHAPES[0][0], "launches": args.steps,
+                          "bytes_per_launch": packed_bytes(C1_SHAPES[0][1], C1_SHAPES[0][2]),
+                          "copy_bytes": COPY_BYTES}), flush=True)
+        return 0
+
     # Timed region: exactly `steps` steps, replayed from one graph (no host
     # launch overhead between kernels), synchronize on both sides.
     steps_graph = graph_of(lambda: [step(s % ring) for s in range(args.steps)])
@@ -176,10 +243,17 @@ def main() -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     del steps_graph
 
-    # Dominant kernel (gate/up): per-launch HIP event pairs on the launch stream.
+    # Dominant kernel (gate/up): `steps` cold launches back to back from one graph,
+    # HIP events around them on the launch stream -> average launch duration.
     dominant = 0
     dom_name, dom_K, dom_N = C1_SHAPES[dominant]
     dom_bytes = packed_bytes(dom_K, dom_N)
+    dom_graph = graph_of(lambda: [tq1_matmul(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant],
+                                             config=config) for s in range(args.steps)])
+    graph_launch_ms = time_graph(dom_graph) / args.steps
+    del dom_graph
+    achieved = dom_bytes / (graph_launch_ms * 1e-3) / 1e9
+    # Eager launches bracketed one by one by event pairs (includes dispatch latency).
     stream = torch.cuda.current_stream(dev)
     pairs = [events() for _ in range(args.steps)]
     for s in range(args.steps):
@@ -190,12 +264,6 @@ def main() -> int:
     launch_ms = sorted(a.elapsed_time(b) for a, b in pairs)
     mean_launch_ms = sum(launch_ms) / len(launch_ms)
     median_launch_ms = launch_ms[len(launch_ms) // 2]
-    achieved = dom_bytes / (mean_launch_ms * 1e-3) / 1e9
-    # Same kernel back to back inside a graph: launch + gap, for comparison.
-    dom_graph = graph_of(lambda: [tq1_matmul(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant],
-                                             config=config) for s in range(args.steps)])
-    graph_launch_ms = time_graph(dom_graph) / args.steps
-    del dom_graph
     per_matrix = {}
     for i, (name, K, N) in enumerate(C1_SHAPES):
         g = graph_of(lambda i=i: [tq1_matmul(weights[s % ring][i], xs[i], layout=layouts[i], config=config)
@@ -207,6 +275,25 @@ def main() -> int:
                              for _ in range(100)])
     warm_ms = time_graph(warm) / 100
     del warm
+
+    # ---- config 2: small batches over the same cold ring (library dispatch) ------
+    small_batch = {}
+    if not args.no_small_batch:
+        for M in SMALL_BATCHES:
+            xm = [synthetic.device_activations(M, K, seed=synthetic.SEED_BASE + 2 + M) for _, K, _ in C1_SHAPES]
+            row = {}
+            for i, (name, K, N) in enumerate(C1_SHAPES):
+                g = graph_of(lambda i=i: [tq1_linear(weights[s % ring][i], xm[i], layout=layouts[i])
+                                          for s in range(ring * 2)])
+                ms = time_graph(g) / (ring * 2)
+                del g
+                row[name] = {"us": round(ms * 1e3, 2),
+                             "GB/s": round(packed_bytes(K, N) / (ms * 1e-3) / 1e9, 1),
+                             "TFLOP/s": round(2 * M * K * N / (ms * 1e-3) / 1e12, 2),
+                             "kernel": select_kernel(layouts[i], M, torch.float16)}
+            small_batch[f"M={M}"] = row
+            del xm
+    traffic = measured_traffic()
 
     result = {
         "metric": "packed-weight GB/s at M=1 (TQ1_G128 decode GEMV, 27B-class shapes)",
@@ -238,30 +325,38 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic["bytes_per_launch"] if traffic else None,
             "kernel": f"{dom_name} GEMV K={dom_K} N={dom_N} (lut_gemv_kernel, fused ordered split-K)",
             "bytes_per_launch": dom_bytes,
-            "mean_launch_us": round(mean_launch_ms * 1e3, 3),
-            "median_launch_us": round(median_launch_ms * 1e3, 3),
-            "graph_back_to_back_us": round(graph_launch_ms * 1e3, 3),
+            "mean_launch_us": round(graph_launch_ms * 1e3, 3),
+            "timing": f"{args.steps} cold launches back to back in one HIP graph, events on the launch stream",
+            "eager_event_pair_mean_us": round(mean_launch_ms * 1e3, 3),
+            "eager_event_pair_median_us": round(median_launch_ms * 1e3, 3),
+            "traffic_detail": traffic,
         },
     }
+    if small_batch:
+        result["small_batch"] = {"workload": "BASELINE configs[2]: M in {2..64} over the three configs[1] "
+                                             "matrices, cold ring, library dispatch (ternel_tq1_linear)",
+                                 **small_batch}
     del weights
 
-    # ---- config 3: prefill GEMM M=512 -------------------------------------------
+    # ---- config 3: prefill GEMM M=512 and M=2048 ---------------------------------
     if not args.no_prefill:
-        prefill = {}
-        for name, K, N in C3_SHAPES:
-            lay = PackedTensorLayout.for_tensor(N, K)
-            blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
-            xp = synthetic.device_activations(512, K, seed=synthetic.SEED_BASE + 3, sigma=0.5)
-            g = graph_of(lambda: [tq1_gemm(blk, xp, layout=lay, config=GemmConfig()) for _ in range(20)])
-            ms = time_graph(g) / 20
-            tflops = 2 * 512 * K * N / (ms * 1e-3) / 1e12
-            prefill[name] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2),
-                             "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
-            del g, blk, xp
-        result["prefill_m512"] = prefill
+        for M in PREFILL_BATCHES:
+            prefill = {}
+            for name, K, N in C3_SHAPES:
+                lay = PackedTensorLayout.for_tensor(N, K)
+                blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
+                xp = synthetic.device_activations(M, K, seed=synthetic.SEED_BASE + 3, sigma=0.5)
+                reps = max(4, 20 * 512 // M)
+                g = graph_of(lambda: [tq1_gemm(blk, xp, layout=lay, config=GemmConfig()) for _ in range(reps)])
+                ms = time_graph(g) / reps
+                tflops = 2 * M * K * N / (ms * 1e-3) / 1e12
+                prefill[name] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2),
+                                 "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+                del g, blk, xp
+            result[f"prefill_m{M}"] = prefill
 
     # ---- config 4: 64-layer weight stream + one embedding row -------------------
     if not args.no_model_stream:
