@@ -167,7 +167,7 @@ def _positional_case(slot: int | None):
 
 
 @pytest.mark.parametrize("slot", [0, 7, 24, None])
-@pytest.mark.parametrize("product", ["reference_gemv", "lut23_matmul", "oracle_matmul"])
+@pytest.mark.parametrize("product", ["reference_gemv", "lut23_matmul", "oracle_matmul", "cpu_decode_matmul"])
 def test_positional_vectors_give_exact_integers(slot, product: str) -> None:
     """tests/test_mlx_kernels.py:107-153 pattern: byte - 121 per slot, byte - 13 for the tail."""
     blocks, x, want = _positional_case(slot)
@@ -179,7 +179,7 @@ def test_positional_vectors_give_exact_integers(slot, product: str) -> None:
     np.testing.assert_array_equal(np.asarray(got, dtype=np.float64), want)
 
 
-@pytest.mark.parametrize("product", ["reference_gemv", "lut23_matmul", "oracle_matmul"])
+@pytest.mark.parametrize("product", ["reference_gemv", "lut23_matmul", "oracle_matmul", "cpu_decode_matmul"])
 def test_small_brute_force_product(product: str) -> None:
     blocks, x, want = SMALL["blocks"], SMALL["x"], SMALL["expected"]
     if product == "reference_gemv":
@@ -209,6 +209,9 @@ def test_three_products_agree_within_fp32_rounding() -> None:
     ref = np.stack([O.reference_gemv(blocks, x[i], rows=rows, columns=columns) for i in range(3)])
     for got in (lut, ref):
         assert O.compare(got, oracle)["normalised_max_abs_error"] < 1e-6
+    # the CPU baseline arm rounds its fp32 product to fp16 once
+    cpu = O.cpu_decode_matmul(blocks, x, rows=rows, columns=columns).astype(np.float64)
+    assert np.all(np.abs(cpu - oracle) <= np.abs(oracle) * 2.0**-11 + 1e-6 * np.abs(oracle).max())
 
 
 def test_get_rows_reference_closed_form() -> None:
