@@ -117,16 +117,26 @@ size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t column
                                          int k_split);
 
 /*
- * MFMA product y = x @ W^T (prefill, and small batches through split-K):
- * trits decoded to fp16 (t-1)*scale tiles in LDS, v_mfma_f32_32x32x16_f16,
- * fp32 accumulation. fp16 activations only (16-byte aligned). Replaces tq1_gemm,
- * src/ternel_mlx/kernels.py:1287-1357. k_split divides columns/128 (0 = auto);
- * ws holds fp32 partials past the same 64 KiB counter region (left untouched),
- * sized by ternel_tq1_gemm_workspace_bytes.
+ * MFMA product y = x @ W^T, fp16 activations, v_mfma_f32_32x32x16_f16 with fp32
+ * accumulation, in one of two forms (the reference's GemmConfig forms,
+ * src/ternel_mlx/kernels.py:1043-1188, re-chosen for CDNA4):
+ *   TERNEL_TQ1_GEMM_TILE   (prefill) 128x128 output tiles, weights decoded to
+ *                          fp16 (t-1)*scale tiles in LDS; x 16-byte aligned;
+ *   TERNEL_TQ1_GEMM_DIRECT (M <= 64) weights decoded straight into MFMA
+ *                          operand registers, activations staged in LDS,
+ *                          split-K reduced in the same launch in chunk order;
+ *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 64, TILE above.
+ * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. k_split divides
+ * columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
+ * same 64 KiB counter region + fp32 partials contract as ternel_tq1_matmul.
  */
+#define TERNEL_TQ1_GEMM_AUTO 0
+#define TERNEL_TQ1_GEMM_TILE 1
+#define TERNEL_TQ1_GEMM_DIRECT 2
 int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
-                    int64_t columns, int dtype, int k_split, void *ws, size_t ws_bytes, void *stream);
-size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int k_split);
+                    int64_t columns, int dtype, int form, int k_split, void *ws, size_t ws_bytes,
+                    void *stream);
+size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int form, int k_split);
 
 /*
  * Packed embedding gather: out[t][c] = (trit(ids[t], c) - 1) * scale for
@@ -139,7 +149,7 @@ int ternel_tq1_get_rows(const uint32_t *packed, int64_t rows, int64_t columns, c
 
 /*
  * packed_matmul dispatch (src/ternel_mlx/modules.py:425-457): the LUT23 path
- * or the MFMA path and its split, from (M, rows, columns, dtype). ws sized by
+ * or an MFMA form and its split, from (M, rows, columns, dtype). ws sized by
  * ternel_tq1_linear_workspace_bytes, same contract as ternel_tq1_matmul's.
  */
 int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,

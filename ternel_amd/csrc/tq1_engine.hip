@@ -142,6 +142,8 @@ __device__ __forceinline__ int64_t packed_word_index(int64_t row, int64_t G, int
 // ---------------------------------------------------------------------------
 // Helpers
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int ceil_div_dev(int a, int b) { return (a + b - 1) / b; }
+
 __global__ void zero_u64_kernel(unsigned long long *p, int n) {
     const int i = threadIdx.x;
     if (i < n) p[i] = 0ull;
@@ -727,6 +729,303 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// direct_gemm_kernel: the "direct fragments" form for small batches (M <= 64).
+//
+// Weights never touch LDS: each lane decodes half of one block straight into
+// the A operand of v_mfma_f32_32x32x16_f16 (weight rows x K); the activations
+// are the B operand (K x batch). A workgroup (4 waves, 128 weight rows) copies
+// its K chunk of activations into LDS once, with LDS-DMA loads (one padded
+// row per instruction, no registers), then each wave runs its groups with no
+// barrier: a wave owns 32 weight rows, lane l decodes half h = l / 32 of row
+// l % 32's block and reads 5 of the block's 7 words. NB = ceil(M / 32) tiles.
+//
+// K order. The dot product over a group does not depend on the order of its
+// 128 terms, so both operands use one fixed permutation that makes the two
+// halves decode with the same code: half h takes code bytes 12h .. 12h+11
+// (trits 60h .. 60h+59) as positions 0..59, then positions 60..63 are trits
+// 120..123 (digits 0-3 of code byte 24) for h = 0, and trits 124..127 (digit 4
+// of code byte 24, the three tail trits) for h = 1. MFMA step s takes positions
+// 8s .. 8s+7 of half h as its K slice 16s + 8h. The activation rows are staged
+// in that order: logical 4-half unit u holds physical unit u (u < 15), 30
+// (u = 15), u - 1 (16 <= u < 31) or 31 (u = 31).
+//
+// Digits. For a byte p <= 242, t = p * 69043 approximates p / 243 in 24-bit
+// fixed point (exact digits for every legal byte, checked exhaustively), and
+// each step t = (t mod 2^24) * 3 -- one v_mul_u32_u24, which ignores the bits
+// above 24 -- leaves the next base-3 digit, most significant first, in bits
+// 24-25. The tail byte (p <= 26) uses 621387 = 9 * 69043. Two such digit
+// carriers become two fp16 weights with two v_perm_b32: one gathers their top
+// bytes, the other selects from {-s, z, +s} as in the LDS-tile form. Illegal
+// bytes give arbitrary digits in 0..2, so nothing is ever indexed by them.
+// ---------------------------------------------------------------------------
+constexpr int kDirectWaves = 4;
+constexpr int kDirectThreads = kDirectWaves * 64;
+constexpr int kDirectRows = kDirectWaves * 32;          // weight rows per workgroup
+constexpr int kDirectLdsBytes = 160 * 1024 - 1024;      // dynamic LDS budget (gfx950: 160 KiB per workgroup)
+constexpr int kDirectStride = kBlockWeights + 8;      // halves per staged activation row
+constexpr uint32_t kByteDigitScale = 69043u;          // ~2^24 / 243
+constexpr uint32_t kTailDigitScale = 9u * 69043u;     // ~2^24 / 27
+
+__device__ __forceinline__ void byte_digit_carriers(uint32_t p, uint32_t (&d)[5]) {
+    uint32_t t = __umul24(p, kByteDigitScale);
+#pragma unroll
+    for (int i = 4; i >= 0; --i) {
+        t = __umul24(t, 3u);
+        d[i] = t;  // digit i (weight 3^i) in bits 24-25
+    }
+}
+
+__device__ __forceinline__ uint32_t weight_pair(uint32_t even, uint32_t odd, uint32_t table_hi, uint32_t table_lo) {
+    const uint32_t pair = __builtin_amdgcn_perm(odd, even, 0x0c070c03u);  // top bytes -> bytes 0 and 2
+    return __builtin_amdgcn_perm(table_hi, table_lo, __umul24(pair, 0x0202u) + 0x01000100u);
+}
+
+
+// One pipeline step of direct_gemm_kernel: the MFMAs of the current group
+// (weights already decoded in a_mfma, activations in LDS buffer `buf`) with the
+// decode of the next group (words u, other -> a_dec) interleaved stage by
+// stage: decode stage st produces exactly the four dwords MFMA step st of the
+// following group will need.
+template <int NB, bool kMfma = true>
+__device__ __forceinline__ void direct_step(float16v (&acc)[NB], const uint32_t (&a_mfma)[32], uint32_t (&a_dec)[32],
+                                            const uint32_t (&u)[4], uint32_t other, bool upper,
+                                            const _Float16 *xb, uint32_t scale_mask = 0xffffu) {
+    // scale_mask 0 turns a padding group's weights into +-0.
+    const uint32_t s = (upper ? other : u[0]) & scale_mask;
+    const uint32_t zero = (s & 0x7c00u) == 0x7c00u ? 0x7e00u : 0u;
+    const uint32_t table_lo = (zero << 16) | (s ^ 0x8000u);
+    const uint32_t table_hi = s;
+    uint32_t c[64];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+        half8 bf[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            bf[nb] = *reinterpret_cast<const half8 *>(xb + nb * 32 * kDirectStride + st * 8);
+        // Bytes whose first position falls in this stage.
+#pragma unroll
+        for (int j = 0; j < 12; ++j) {
+            if ((5 * j) / 8 != st) continue;
+            const int b = 2 + j;
+            uint32_t d[5];
+            byte_digit_carriers((u[b >> 2] >> (8 * (b & 3))) & 0xffu, d);
+#pragma unroll
+            for (int i = 0; i < 5; ++i) c[5 * j + i] = d[i];
+        }
+        if (st == 7) {
+            const uint32_t w6 = upper ? u[3] : other;
+            uint32_t d24[5];
+            byte_digit_carriers((w6 >> 16) & 0xffu, d24);
+            uint32_t t = __umul24(w6 >> 24, kTailDigitScale);
+            const uint32_t t2 = t = __umul24(t, 3u);
+            const uint32_t t1 = t = __umul24(t, 3u);
+            const uint32_t t0 = __umul24(t, 3u);
+            c[60] = upper ? d24[4] : d24[0];
+            c[61] = upper ? t0 : d24[1];
+            c[62] = upper ? t1 : d24[2];
+            c[63] = upper ? t2 : d24[3];
+        }
+#pragma unroll
+        for (int p = 4 * st; p < 4 * st + 4; ++p) a_dec[p] = weight_pair(c[2 * p], c[2 * p + 1], table_hi, table_lo);
+        if (!kMfma) continue;
+        half8 af;
+        {
+            uint4 v = {a_mfma[4 * st], a_mfma[4 * st + 1], a_mfma[4 * st + 2], a_mfma[4 * st + 3]};
+            af = *reinterpret_cast<half8 *>(&v);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[nb], 0, 0, 0);
+    }
+}
+
+// MFMA steps of one group with weights already decoded (no decode).
+template <int NB>
+__device__ __forceinline__ void direct_mfma(float16v (&acc)[NB], const uint32_t (&a)[32], const _Float16 *xb) {
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+        half8 af;
+        {
+            uint4 v = {a[4 * st], a[4 * st + 1], a[4 * st + 2], a[4 * st + 3]};
+            af = *reinterpret_cast<half8 *>(&v);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const half8 bf = *reinterpret_cast<const half8 *>(xb + nb * 32 * kDirectStride + st * 8);
+            acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[nb], 0, 0, 0);
+        }
+    }
+}
+
+// Logical 4-half unit u of a staged activation row holds physical unit
+// direct_source_unit(u) of the group (the K order above).
+__device__ __forceinline__ int direct_source_unit(int u) { return u < 15 ? u : (u == 15 ? 30 : (u < 31 ? u - 1 : 31)); }
+
+template <int NB, int SR>
+__global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
+    const uint32_t *__restrict__ packed, const _Float16 *__restrict__ x, _Float16 *__restrict__ y,
+    float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
+    int k_split, int window) {
+    static_assert(SR <= 32 * NB && SR >= 8, "staged rows");
+    extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // window x SR rows x kDirectStride halves
+    __shared__ unsigned s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const bool upper = lane >= 32;
+    const int row0 = blockIdx.x * kDirectRows + wave * 32;
+    const int g_begin = blockIdx.y * chunk_groups;
+    const int cg = chunk_groups;
+    const int64_t K = static_cast<int64_t>(G) * kBlockWeights;
+
+    // Rows past the padded last tile load the last padded row (discarded).
+    const int load_row = min(row0 + (lane & 31), ceil_div_dev(N, kTileRows) * kTileRows - 1);
+    const uint32_t *wrow = packed + static_cast<int64_t>(load_row / kTileRows) * G * kTileGroupWords + (load_row % kTileRows);
+    const int wfirst = (upper ? 3 : 0) * kTileRows;
+    const int wother = (upper ? 0 : 6) * kTileRows;
+
+    // LDS-DMA staging of one activation row per instruction: lane l fetches
+    // logical dword l of the row (physical unit direct_source_unit(l / 2)), the
+    // hardware writes it at row base + 4 l. Rows past M re-read row M - 1.
+    const int src_half = direct_source_unit(lane >> 1) * 4 + (lane & 1) * 2;
+    // B fragments: activation row (lane & 31) (+32 for the second tile); rows
+    // past SR read row SR - 1 (their MFMA columns are never stored).
+    const int brow = min(lane & 31, SR - 1);
+    const int bofs = brow * kDirectStride + (upper ? 64 : 0);
+
+    float16v acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
+
+    constexpr int CH = 4;  // groups of words per prefetch set
+    for (int w0 = 0; w0 < cg; w0 += window) {
+        const int wn = min(window, cg - w0);
+        const int gw = g_begin + w0;
+        auto load_chunk = [&](uint32_t (&w)[CH][5], int q) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const uint32_t *p = wrow + static_cast<int64_t>(gw + min(q + c, wn - 1)) * kTileGroupWords;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[c][j] = p[wfirst + j * kTileRows];
+                w[c][4] = p[wother];
+            }
+        };
+        auto xb = [&](int q) { return xs + q * SR * kDirectStride + bofs; };
+
+        if (w0) __syncthreads();  // every wave is done with the previous window's activations
+        uint32_t wa[CH][5], wb[CH][5];
+        load_chunk(wa, 0);
+        load_chunk(wb, CH);
+        for (int r = wave; r < wn * SR; r += kDirectWaves) {
+            const int q = r / SR, m = r - q * SR;
+            const _Float16 *src = x + static_cast<int64_t>(min(m, M - 1)) * K + static_cast<int64_t>(gw + q) * kBlockWeights + src_half;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                             (__attribute__((address_space(3))) void *)(xs + r * kDirectStride), 4, 0, 0);
+        }
+        wait_vector_memory();
+        __syncthreads();
+
+        // Pipeline over the window (no barriers): MFMAs of group q interleaved
+        // with the decode of q+1; words come in sets of four groups issued four
+        // steps before their first decode. Decoded weights alternate with
+        // period 2 and word sets with period 8, so the loop body is 8 steps and
+        // no register is copied (a copy would wait for its prefetch).
+        uint32_t a0[32], a1[32];
+        {
+            const uint32_t u[4] = {wa[0][0], wa[0][1], wa[0][2], wa[0][3]};
+            direct_step<NB, false>(acc, a1, a0, u, wa[0][4], upper, xb(0));
+        }
+        auto step = [&](const uint32_t (&a_mfma)[32], uint32_t (&a_dec)[32], const uint32_t (&w)[5], int q) {
+            const uint32_t u[4] = {w[0], w[1], w[2], w[3]};
+            direct_step<NB>(acc, a_mfma, a_dec, u, w[4], upper, xb(q));
+        };
+        int q = 0;
+        for (; q + 2 * CH <= wn; q += 2 * CH) {
+            step(a0, a1, wa[1], q + 0);
+            step(a1, a0, wa[2], q + 1);
+            step(a0, a1, wa[3], q + 2);
+            step(a1, a0, wb[0], q + 3);
+            // The fences keep the scheduler from sinking the prefetch toward its use.
+            __builtin_amdgcn_sched_barrier(0);
+            load_chunk(wa, q + 2 * CH);
+            __builtin_amdgcn_sched_barrier(0);
+            step(a0, a1, wb[1], q + 4);
+            step(a1, a0, wb[2], q + 5);
+            step(a0, a1, wb[3], q + 6);
+            step(a1, a0, wa[0], q + 7);
+            __builtin_amdgcn_sched_barrier(0);
+            load_chunk(wb, q + 3 * CH);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // Remainder (fewer than 8 groups): a0 holds group q decoded.
+        for (; q < wn; ++q) {
+            direct_mfma<NB>(acc, a0, xb(q));
+            if (q + 1 < wn) {
+                const uint32_t *p = wrow + static_cast<int64_t>(gw + q + 1) * kTileGroupWords;
+                const uint32_t u[4] = {p[wfirst], p[wfirst + kTileRows], p[wfirst + 2 * kTileRows], p[wfirst + 3 * kTileRows]};
+                direct_step<NB, false>(acc, a1, a0, u, p[wother], upper, xb(q + 1));
+            }
+        }
+    }
+
+    // D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) % 2), item 4 * (i / 8) + i % 4;
+    // here i is a weight row of the wave and j an activation row.
+    if (k_split > 1) {
+        // Partials in fragment order (coalesced, each lane re-reads its own).
+        constexpr int kFrag = NB * 16 * 64;
+        float *mine = partial + ((static_cast<int64_t>(blockIdx.x) * k_split + blockIdx.y) * kDirectWaves + wave) * kFrag + lane;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                __hip_atomic_store(mine + (nb * 16 + r) * 64, acc[nb][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vector_memory();
+        __syncthreads();
+        unsigned *counter = counters + blockIdx.x;
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     static_cast<unsigned>(k_split - 1);
+        __syncthreads();
+        if (!s_last) return;
+        const float *base = partial + (static_cast<int64_t>(blockIdx.x) * k_split * kDirectWaves + wave) * kFrag + lane;
+        const int64_t chunk_stride = static_cast<int64_t>(kDirectWaves) * kFrag;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
+        for (int z = 0; z < k_split; ++z) {
+            float v[NB][16];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    v[nb][r] = __hip_atomic_load(base + z * chunk_stride + (nb * 16 + r) * 64, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[nb][r] += v[nb][r];
+        }
+        if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int m = nb * 32 + (lane & 31);
+        if (m >= M) continue;
+        _Float16 *yrow = y + static_cast<int64_t>(m) * N;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = row0 + 8 * q + 4 * (lane >> 5);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n + e < N) yrow[n + e] = static_cast<_Float16>(acc[nb][4 * q + e]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side geometry
 // ---------------------------------------------------------------------------
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -783,7 +1082,10 @@ bool lut_chunk_supported(int batch_tile, int chunk) {
 
 int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split, LutPlan *plan) {
     const int64_t G = columns / kBlockWeights;
-    if (batch_tile == 0) batch_tile = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
+    // Measured on MI355X: one vector per workgroup beats batch tiles of 2 and 4
+    // at every 27B shape up to M = 4 (gate/up M=4: 18.3 us vs 20.3 and 25.8);
+    // the extra tables and lookups cost more than re-reading the weights from L2.
+    if (batch_tile == 0) batch_tile = 1;
     if (batch_tile != 1 && batch_tile != 2 && batch_tile != 4)
         return fail(TERNEL_TQ1_EINVAL, "batch tile must be 1, 2 or 4, got %d", batch_tile);
     plan->batch_tile = batch_tile;
@@ -924,8 +1226,107 @@ int launch_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, int64
     return TERNEL_TQ1_OK;
 }
 
+// Direct-fragment form: at most 64 activation rows (two 32-wide MFMA tiles).
+constexpr int64_t kDirectMaxBatch = 64;
+// Auto split: at least this many workgroups (4 waves each) to fill 256 CUs twice.
+constexpr int64_t kDirectTargetWorkgroups = 512;
+
+struct DirectPlan {
+    int nb;
+    int staged_rows;
+    int k_split;
+    int chunk_groups;
+    int window;  // groups of activations staged in LDS at once
+    int64_t row_blocks;
+    size_t lds_bytes;
+    size_t partial_bytes;
+};
+
+int direct_staged_rows(int64_t M) { return M <= 8 ? 8 : (M <= 16 ? 16 : (M <= 32 ? 32 : 64)); }
+
+int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPlan *plan) {
+    const int64_t G = columns / kBlockWeights;
+    if (M > kDirectMaxBatch)
+        return fail(TERNEL_TQ1_EINVAL, "the direct-fragment form takes at most %lld activation rows, got %lld",
+                    static_cast<long long>(kDirectMaxBatch), static_cast<long long>(M));
+    plan->nb = M > 32 ? 2 : 1;
+    plan->staged_rows = direct_staged_rows(M);
+    plan->row_blocks = ceil_div(rows, kDirectRows);
+    if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
+    if (k_split == 0) {
+        // Measured on MI355X: chunks of a multiple of 8 groups keep the whole
+        // K chunk in the 8-step pipeline; take the smallest such split that
+        // reaches the workgroup target, else the largest such split.
+        int best = 0;
+        for (int64_t k = 1; k <= G; ++k) {
+            if (G % k || (G / k) % 8) continue;
+            best = static_cast<int>(k);
+            if (plan->row_blocks * k >= kDirectTargetWorkgroups) break;
+        }
+        k_split = best ? best : largest_divisor_split(G, plan->row_blocks, kDirectTargetWorkgroups);
+    }
+    if (G % k_split)
+        return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row", k_split,
+                    static_cast<long long>(G));
+    if (k_split > 65535) return fail(TERNEL_TQ1_EINVAL, "K too large for one launch");
+    if (k_split > 1 && plan->row_blocks > kCounterSlots)
+        return fail(TERNEL_TQ1_EINVAL, "%lld row blocks exceed the %d split-K counters",
+                    static_cast<long long>(plan->row_blocks), kCounterSlots);
+    plan->k_split = k_split;
+    plan->chunk_groups = static_cast<int>(G / k_split);
+    const size_t group_bytes = static_cast<size_t>(plan->staged_rows) * kDirectStride * sizeof(_Float16);
+    int window = static_cast<int>(kDirectLdsBytes / group_bytes);
+    if (window >= plan->chunk_groups)
+        window = plan->chunk_groups;
+    else if (window >= 8)
+        window -= window % 8;
+    plan->window = window;
+    plan->lds_bytes = static_cast<size_t>(window) * group_bytes;
+    plan->partial_bytes = k_split > 1 ? static_cast<size_t>(k_split) * plan->row_blocks * kDirectRows * 32 *
+                                            plan->nb * sizeof(float)
+                                      : 0;
+    return TERNEL_TQ1_OK;
+}
+
+template <int NB, int SR>
+int launch_direct_kernel(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int G,
+                         const DirectPlan &plan, float *partial, unsigned *counters, hipStream_t stream) {
+    static bool attribute_set = false;  // dynamic LDS above 64 KiB needs the opt-in once per kernel
+    if (!attribute_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&direct_gemm_kernel<NB, SR>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kDirectLdsBytes);
+        if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attribute_set = true;
+    }
+    const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.k_split));
+    hipLaunchKernelGGL((direct_gemm_kernel<NB, SR>), grid, dim3(kDirectThreads), plan.lds_bytes, stream, packed,
+                       static_cast<const _Float16 *>(x), static_cast<_Float16 *>(y), partial, counters,
+                       static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split, plan.window);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+int launch_direct(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+                  const DirectPlan &plan, void *ws, hipStream_t stream) {
+    unsigned *counters = plan.k_split > 1 ? static_cast<unsigned *>(ws) : nullptr;
+    float *partial =
+        plan.k_split > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes) : nullptr;
+    const int G = static_cast<int>(columns / kBlockWeights);
+    switch (plan.staged_rows) {
+        case 8: return launch_direct_kernel<1, 8>(packed, x, y, M, rows, G, plan, partial, counters, stream);
+        case 16: return launch_direct_kernel<1, 16>(packed, x, y, M, rows, G, plan, partial, counters, stream);
+        case 32: return launch_direct_kernel<1, 32>(packed, x, y, M, rows, G, plan, partial, counters, stream);
+        default: return launch_direct_kernel<2, 64>(packed, x, y, M, rows, G, plan, partial, counters, stream);
+    }
+}
+
+int resolve_gemm_form(int64_t M, int form) {
+    if (form == TERNEL_TQ1_GEMM_AUTO) return M <= kDirectMaxBatch ? TERNEL_TQ1_GEMM_DIRECT : TERNEL_TQ1_GEMM_TILE;
+    return form;
+}
+
 // The dispatch rule of packed_matmul, retuned for MI355X: the LUT23 kernel up
-// to this many activation rows, the MFMA kernel above it (fp16 only).
+// to this many activation rows, the MFMA kernels above it (fp16 only).
 constexpr int64_t kLinearLutMaxBatch = 4;
 
 int check_packed_pointer(const void *packed) {
@@ -1047,8 +1448,15 @@ int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M,
     }
 }
 
-size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int k_split) {
+size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
+    form = resolve_gemm_form(M, form);
+    if (form == TERNEL_TQ1_GEMM_DIRECT) {
+        DirectPlan direct;
+        if (plan_direct(M, rows, columns, k_split, &direct) != TERNEL_TQ1_OK) return 0;
+        return direct.k_split > 1 ? kCounterRegionBytes + direct.partial_bytes : 0;
+    }
+    if (form != TERNEL_TQ1_GEMM_TILE) return 0;
     GemmPlan plan;
     if (plan_gemm(M, rows, columns, k_split, &plan) != TERNEL_TQ1_OK) return 0;
     return plan.k_split > 1 ? kCounterRegionBytes + static_cast<size_t>(plan.k_split) * M * rows * sizeof(float)
@@ -1056,12 +1464,27 @@ size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns,
 }
 
 int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
-                    int dtype, int k_split, void *ws, size_t ws_bytes, void *stream) {
+                    int dtype, int form, int k_split, void *ws, size_t ws_bytes, void *stream) {
     g_last_error[0] = '\0';
     int rc;
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if (dtype != TERNEL_TQ1_F16)
         return fail(TERNEL_TQ1_EINVAL, "the MFMA path takes fp16 activations, got dtype code %d", dtype);
+    if (form != TERNEL_TQ1_GEMM_AUTO && form != TERNEL_TQ1_GEMM_TILE && form != TERNEL_TQ1_GEMM_DIRECT)
+        return fail(TERNEL_TQ1_EINVAL, "unknown GEMM form %d", form);
+    form = resolve_gemm_form(M, form);
+    if (form == TERNEL_TQ1_GEMM_DIRECT) {
+        DirectPlan direct;
+        if ((rc = plan_direct(M, rows, columns, k_split, &direct)) != TERNEL_TQ1_OK) return rc;
+        if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+        if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+        if (reinterpret_cast<uintptr_t>(x) & 7u) return fail(TERNEL_TQ1_EINVAL, "activations must be 8-byte aligned");
+        const size_t need = direct.k_split > 1 ? kCounterRegionBytes + direct.partial_bytes : 0;
+        if (need && (!ws || ws_bytes < need))
+            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
+                        need);
+        return launch_direct(packed, x, y, M, rows, columns, direct, ws, static_cast<hipStream_t>(stream));
+    }
     GemmPlan plan;
     if ((rc = plan_gemm(M, rows, columns, k_split, &plan)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
@@ -1114,14 +1537,14 @@ int ternel_tq1_get_rows(const uint32_t *packed, int64_t rows, int64_t columns, c
 size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
         return ternel_tq1_matmul_workspace_bytes(M, rows, columns, 0, 0);
-    return ternel_tq1_gemm_workspace_bytes(M, rows, columns, 0);
+    return ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
 }
 
 int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
                       int dtype, void *ws, size_t ws_bytes, void *stream) {
     if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
         return ternel_tq1_matmul(packed, x, y, M, rows, columns, dtype, 0, 0, ws, ws_bytes, stream);
-    return ternel_tq1_gemm(packed, x, y, M, rows, columns, dtype, 0, ws, ws_bytes, stream);
+    return ternel_tq1_gemm(packed, x, y, M, rows, columns, dtype, TERNEL_TQ1_GEMM_AUTO, 0, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

@@ -38,8 +38,8 @@ LUT23_BATCH_TILES = (1, 2, 4)
 class MatmulConfig:
     """LUT23 knobs (src/ternel_mlx/kernels.py:963-1006): batch tile and K split.
 
-    ``0`` means automatic: the batch tile follows the batch (1, 2 or 4) and the
-    split the largest chunk that still fills the 256 CUs.
+    ``0`` means automatic: a batch tile of 1 (fastest at every measured 27B
+    shape) and the split measured best for the shape's groups per row.
     """
 
     batch_tile: int = 0
@@ -57,19 +57,34 @@ class MatmulConfig:
         return name if self.k_split in (0, 1) else f"{name}_k{self.k_split}"
 
 
+GEMM_FORMS = {"auto": 0, "tile": 1, "direct": 2}
+DIRECT_MAX_BATCH = 64
+
+
 @dataclass(frozen=True)
 class GemmConfig:
-    """MFMA prefill knobs: the K split (0 = automatic)."""
+    """MFMA knobs: the kernel form and the K split (0 = automatic).
+
+    ``form`` picks how weight fragments reach the matrix cores, like the
+    reference's ``direct_fragments`` switch (src/ternel_mlx/kernels.py:1043-1188):
+    ``"tile"`` decodes 128x128 weight tiles into LDS (prefill), ``"direct"``
+    decodes straight into MFMA operand registers (at most 64 activation rows),
+    ``"auto"`` takes ``"direct"`` up to 64 rows and ``"tile"`` above.
+    """
 
     k_split: int = 0
+    form: str = "auto"
 
     def __post_init__(self) -> None:
         if self.k_split < 0:
             raise FormatError(f"k split must be positive, got {self.k_split}")
+        if self.form not in GEMM_FORMS:
+            raise FormatError(f"GEMM form must be one of {sorted(GEMM_FORMS)}, got {self.form!r}")
 
     @property
     def benchmark_name(self) -> str:
-        return "gemm_128x128" if self.k_split in (0, 1) else f"gemm_128x128_k{self.k_split}"
+        name = "gemm_128x128" if self.form == "tile" else f"gemm_{self.form}"
+        return name if self.k_split in (0, 1) else f"{name}_k{self.k_split}"
 
 
 def _stream(device: torch.device) -> int:
@@ -195,14 +210,17 @@ def tq1_gemm(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayou
         raise FormatError(
             f"k split {config.k_split} does not divide the tensor's {layout.groups_per_row} groups per row"
         )
+    if config.form == "direct" and batch > DIRECT_MAX_BATCH:
+        raise FormatError(f"the direct-fragment form takes at most {DIRECT_MAX_BATCH} activation rows, got {batch}")
+    form = GEMM_FORMS[config.form]
     x = x.contiguous()
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
-    need = handle.ternel_tq1_gemm_workspace_bytes(batch, layout.rows, layout.columns, config.k_split)
+    need = handle.ternel_tq1_gemm_workspace_bytes(batch, layout.rows, layout.columns, form, config.k_split)
     ws = workspace(x.device, need)
     _lib.check(handle.ternel_tq1_gemm(
         packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns,
-        _lib.DTYPE_F16, config.k_split, ws.data_ptr() if ws is not None else None,
+        _lib.DTYPE_F16, form, config.k_split, ws.data_ptr() if ws is not None else None,
         ws.numel() if ws is not None else 0, _stream(x.device)))
     return out
 

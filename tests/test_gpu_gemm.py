@@ -1,4 +1,5 @@
-"""MFMA prefill kernel against the fp64 oracle.
+"""Both MFMA forms (LDS weight tiles; weights decoded into operand registers)
+against the fp64 oracle.
 
 Weights decode to fp16 (t - 1) * scale exactly and fp16 x fp16 products are
 exact in fp32, so the only roundings are the fp32 accumulation and the final
@@ -24,9 +25,13 @@ NORTH_STAR_TOLERANCE = 1e-3
 FP16_UNIT_ROUNDOFF = 2.0 ** -11
 
 
-def run(blocks: np.ndarray, x16: np.ndarray, *, k_split: int = 0) -> np.ndarray:
+FORMS = ("tile", "direct")
+
+
+def run(blocks: np.ndarray, x16: np.ndarray, *, k_split: int = 0, form: str = "auto") -> np.ndarray:
     rows, g, _ = blocks.shape
-    out = tq1_gemm(pack(blocks), to_dev(x16), layout=layout(rows, g * 128), config=GemmConfig(k_split=k_split))
+    out = tq1_gemm(pack(blocks), to_dev(x16), layout=layout(rows, g * 128),
+                   config=GemmConfig(k_split=k_split, form=form))
     torch.cuda.synchronize()
     return out.float().cpu().numpy().astype(np.float64)
 
@@ -47,39 +52,50 @@ def assert_fp16_faithful(got: np.ndarray, blocks: np.ndarray, x16: np.ndarray) -
     assert result["pattern_mismatches"] == 0
 
 
-def test_mfma_lane_layout_probe() -> None:
-    """Identity activations pick out single weights: y[m][n] = W[n][m] for m < 128.
+@pytest.mark.parametrize("form", FORMS)
+@pytest.mark.parametrize("offset", (0, 64))
+def test_mfma_lane_layout_probe(form: str, offset: int) -> None:
+    """Identity activations pick out single weights: y[m][n] = W[n][offset + m].
 
-    A transposed operand or a wrong accumulator lane map moves values to other
-    positions, which this catches element by element.
+    A transposed operand, a wrong accumulator lane map or (direct form) a K
+    order of the activations that differs from the weights' moves values to
+    other positions, which this catches element by element.
     """
-    rows, columns = 256, 128
+    rows, columns = 256, 256
     blocks = random_blocks(rows, columns, seed=11)
-    x = np.eye(128, columns, dtype=np.float16)
-    got = run(blocks, x)
+    x = np.zeros((64, columns), dtype=np.float16)
+    x[np.arange(64), offset + np.arange(64)] = 1.0
+    x[np.arange(64), 128 + offset + np.arange(64)] = 1.0  # second group: same positions
+    got = run(blocks, x, form=form)
     weights = O.dense_weights(blocks, rows=rows, columns=columns).astype(np.float16).astype(np.float64)
-    np.testing.assert_array_equal(got, weights.T[:128])
+    want = (weights[:, offset:offset + 64] + weights[:, 128 + offset:128 + offset + 64]).T
+    np.testing.assert_array_equal(got, want.astype(np.float16).astype(np.float64))
 
 
 SHAPES = ((48, 5120), (256, 640), (512, 384), (1024, 5120), (300, 256))
 
 
+@pytest.mark.parametrize("form", FORMS)
 @pytest.mark.parametrize(("rows", "columns"), SHAPES)
-@pytest.mark.parametrize("batch", (1, 5, 33, 64, 130, 256))
-def test_gemm_matches_the_oracle(rows: int, columns: int, batch: int) -> None:
+@pytest.mark.parametrize("batch", (1, 5, 32, 33, 64, 130, 256))
+def test_gemm_matches_the_oracle(form: str, rows: int, columns: int, batch: int) -> None:
+    if form == "direct" and batch > 64:
+        pytest.skip("the direct form takes at most 64 activation rows")
     blocks = random_blocks(rows, columns, seed=rows * 31 + columns)
     x = np.random.default_rng(rows + columns + batch).normal(0.0, 1.0, size=(batch, columns)).astype(np.float16)
-    assert_fp16_faithful(run(blocks, x), blocks, x)
+    assert_fp16_faithful(run(blocks, x, form=form), blocks, x)
 
 
+@pytest.mark.parametrize("form", FORMS)
 @pytest.mark.parametrize("k_split", (1, 2, 5, 8, 40))
-def test_gemm_split_k_matches_the_oracle(k_split: int) -> None:
+def test_gemm_split_k_matches_the_oracle(form: str, k_split: int) -> None:
     blocks = random_blocks(384, 5120, seed=k_split)
     x = np.random.default_rng(k_split).normal(0.0, 0.5, size=(37, 5120)).astype(np.float16)
-    assert_fp16_faithful(run(blocks, x, k_split=k_split), blocks, x)
+    assert_fp16_faithful(run(blocks, x, k_split=k_split, form=form), blocks, x)
 
 
-def test_gemm_split_k_is_exact_on_integer_data() -> None:
+@pytest.mark.parametrize("form", FORMS)
+def test_gemm_split_k_is_exact_on_integer_data(form: str) -> None:
     rows, groups = 256, 40
     rng = np.random.default_rng(3)
     scales = np.full(rows * groups, 1.0, dtype=np.float16).view(np.uint8).reshape(-1, 2)
@@ -91,24 +107,26 @@ def test_gemm_split_k_is_exact_on_integer_data() -> None:
     # compare through fp16 rounding of the exact answer.
     want16 = want.astype(np.float16).astype(np.float64)
     for k in (1, 2, 4, 5, 8, 10, 20, 40):
-        np.testing.assert_array_equal(run(blocks, x, k_split=k), want16, err_msg=f"k_split={k}")
+        np.testing.assert_array_equal(run(blocks, x, k_split=k, form=form), want16, err_msg=f"k_split={k}")
 
 
-def test_gemm_is_deterministic() -> None:
+@pytest.mark.parametrize("form", FORMS)
+def test_gemm_is_deterministic(form: str) -> None:
     blocks = random_blocks(512, 5120, seed=5)
     x = np.random.default_rng(5).normal(0, 1, size=(64, 5120)).astype(np.float16)
-    first = run(blocks, x, k_split=8)
+    first = run(blocks, x, k_split=8, form=form)
     for _ in range(2):
-        np.testing.assert_array_equal(run(blocks, x, k_split=8), first)
+        np.testing.assert_array_equal(run(blocks, x, k_split=8, form=form), first)
 
 
-def test_gemm_propagates_non_finite_activations() -> None:
+@pytest.mark.parametrize("form", FORMS)
+def test_gemm_propagates_non_finite_activations(form: str) -> None:
     blocks = random_blocks(256, 384, seed=7)
     x = np.zeros((3, 384), dtype=np.float16)
     x[0, 0] = np.nan
     x[1, 125] = np.inf
     x[2, 383] = -np.inf
-    got = run(blocks, x)
+    got = run(blocks, x, form=form)
     want = O.oracle_matmul(blocks, x.astype(np.float64), rows=256, columns=384)
     assert O.compare(got, want)["pattern_mismatches"] == 0
 
@@ -123,3 +141,23 @@ def test_gemm_rejects_other_dtypes_and_bad_splits() -> None:
                  config=GemmConfig(k_split=2))
     with pytest.raises(FormatError, match="activations have 256 columns, expected 384"):
         tq1_gemm(blocks, torch.zeros((4, 256), device="cuda", dtype=torch.float16), layout=lay)
+    with pytest.raises(FormatError, match="at most 64 activation rows"):
+        tq1_gemm(blocks, torch.zeros((65, 384), device="cuda", dtype=torch.float16), layout=lay,
+                 config=GemmConfig(form="direct"))
+
+
+@pytest.mark.parametrize("form", FORMS)
+def test_gemm_non_finite_scales_follow_ieee(form: str) -> None:
+    """A zero trit times an inf/NaN scale is NaN, as (t - 1) * scale computes it."""
+    rows, columns = 128, 256
+    rng = np.random.default_rng(9)
+    scale_values = np.full(rows * 2, 0.5, dtype=np.float16)
+    scale_values[3] = np.inf
+    scale_values[64] = -np.inf
+    scale_values[130] = np.nan
+    trits = rng.integers(0, 3, size=(rows * 2, 128), dtype=np.uint8)
+    blocks = O.encode_tq1_blocks(scale_values.view(np.uint8).reshape(-1, 2), trits).reshape(rows, 2, 28)
+    x = rng.normal(0, 1, size=(4, columns)).astype(np.float16)
+    got = run(blocks, x, form=form)
+    want = O.oracle_matmul(blocks, x.astype(np.float64), rows=rows, columns=columns)
+    assert O.compare(got, want)["pattern_mismatches"] == 0

@@ -180,8 +180,12 @@ def test_argument_errors_are_reported_without_a_launch() -> None:
     assert rc == _lib.TERNEL_TQ1_EINVAL
     # geometry passes, then the null pointers are refused
     assert "null pointer" in _lib.last_error() or "does not divide" in _lib.last_error()
-    rc = handle.ternel_tq1_gemm(None, None, None, 4, 256, 5120, 2, 0, None, 0, None)
+    rc = handle.ternel_tq1_gemm(None, None, None, 4, 256, 5120, 2, 0, 0, None, 0, None)
     assert rc == _lib.TERNEL_TQ1_EINVAL and "fp16" in _lib.last_error()
+    rc = handle.ternel_tq1_gemm(None, None, None, 4, 256, 5120, 0, 7, 0, None, 0, None)
+    assert rc == _lib.TERNEL_TQ1_EINVAL and "unknown GEMM form 7" in _lib.last_error()
+    rc = handle.ternel_tq1_gemm(None, None, None, 65, 256, 5120, 0, 2, 0, None, 0, None)
+    assert rc == _lib.TERNEL_TQ1_EINVAL and "at most 64 activation rows" in _lib.last_error()
     rc = handle.ternel_tq1_get_rows(None, 256, 5120, None, 0, None, 0, None)
     assert rc == _lib.TERNEL_TQ1_EINVAL and "indices are empty" in _lib.last_error()
 
@@ -199,8 +203,15 @@ def test_workspace_queries() -> None:
     counters = 64 * 1024  # fixed split-K counter region at the front of every workspace
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 1) == 0
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 8) == counters + 8 * 256 * 4
-    assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, 1) == 0
-    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, 5) == counters + 5 * 8 * 256 * 4
+    tile, direct = 1, 2
+    assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, tile, 1) == 0
+    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, tile, 5) == counters + 5 * 8 * 256 * 4
+    assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, 0, 1) == 0  # auto -> tile
+    # direct form: partials are 128 rows x 32 (or 64) activation columns per row block and chunk
+    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, direct, 1) == 0
+    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, direct, 5) == counters + 5 * 2 * 128 * 32 * 4
+    assert handle.ternel_tq1_gemm_workspace_bytes(40, 300, 5120, direct, 4) == counters + 4 * 3 * 128 * 64 * 4
+    assert handle.ternel_tq1_gemm_workspace_bytes(65, 256, 5120, direct, 1) == 0  # rejected
     assert handle.ternel_tq1_packed_words(300, 640) == 5 * 5 * 7 * 64
     assert handle.ternel_tq1_packed_words(300, 600) == 0
 
