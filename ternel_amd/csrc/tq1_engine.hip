@@ -462,41 +462,35 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
         build_lut_tables<T, C, BT>(lut, xv, tid);
         __syncthreads();
 
-        // 3. Consume (rows past N compute a discarded value). The C blocks are
-        //    walked word by word together, giving C independent add chains to
-        //    hide LDS latency; within a block the order is slot 0..24, tail,
-        //    then one fma with the scale, and blocks fold into acc in order.
-        {
-            float sum[C][BT];
+        // 3. Consume (rows past N compute a discarded value), block by block in
+        //    load order, so block c is summed while blocks c+1.. are still
+        //    arriving (loads complete in order). Within a block: slot 0..24,
+        //    the tail, then one fma with the scale; blocks fold into acc in
+        //    order -- the reference's summation order.
 #pragma unroll
-            for (int c = 0; c < C; ++c)
+        for (int c = 0; c < C; ++c) {
+            float sum[BT];
 #pragma unroll
-                for (int j = 0; j < BT; ++j) sum[c][j] = 0.0f;
+            for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
 #pragma unroll
             for (int word = 0; word < kBlockWords; ++word) {
+                uint32_t lo[4], hi[4];
+                split_word(w[c][word], lo, hi);
 #pragma unroll
-                for (int c = 0; c < C; ++c) {
-                    uint32_t lo[4], hi[4];
-                    split_word(w[c][word], lo, hi);
+                for (int b = 0; b < 4; ++b) {
+                    const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
+                    if (s < 0 || s >= kFullSlots) continue;
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
-                        if (s < 0 || s >= kFullSlots) continue;
-#pragma unroll
-                        for (int j = 0; j < BT; ++j)
-                            sum[c][j] += lut[j][c][s * kL2Entries + lo[b]] + lut[j][c][kL3Base + s * kL3Entries + hi[b]];
-                    }
+                    for (int j = 0; j < BT; ++j)
+                        sum[j] += lut[j][c][s * kL2Entries + lo[b]] + lut[j][c][kL3Base + s * kL3Entries + hi[b]];
                 }
             }
+            const float scale = half_bits_to_float(w[c][0]);
+            const uint32_t tail = min(w[c][6] >> 24, kMaxTailByte);
 #pragma unroll
-            for (int c = 0; c < C; ++c) {
-                const float scale = half_bits_to_float(w[c][0]);
-                const uint32_t tail = min(w[c][6] >> 24, kMaxTailByte);
-#pragma unroll
-                for (int j = 0; j < BT; ++j) {
-                    sum[c][j] += lut[j][c][kTailBase + tail];
-                    acc[j] = fmaf(scale, sum[c][j], acc[j]);
-                }
+            for (int j = 0; j < BT; ++j) {
+                sum[j] += lut[j][c][kTailBase + tail];
+                acc[j] = fmaf(scale, sum[j], acc[j]);
             }
         }
     }
@@ -570,31 +564,64 @@ constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
 constexpr int kGemmStride = kBlockWeights + 8;  // halves per LDS row
 
-// Decodes weights k = 64H .. 64H+63 of one block into 32 dwords = 64 fp16
-// (t - 1) * scale values in k order. Digits come from a mul-shift chain
-// (q / 3 == (q * 171) >> 9 for q < 256); each pair of adjacent weights is one
-// v_perm_b32 byte select from the 8-byte table {-s, z, +s}, selector
-// d * 0x202 + 0x100 per half. z is 0, or NaN when the scale is inf/NaN, so
-// that (t - 1) * s keeps IEEE semantics (0 * inf = NaN) exactly.
+// Digit carriers (see the direct-fragment form below for the method): for a
+// byte p <= 242, t = p * 69043 approximates p / 243 in 24-bit fixed point and
+// each t = (t mod 2^24) * 3 leaves the next base-3 digit, most significant
+// first, in bits 24-25 (exact for every legal byte; the tail byte p <= 26 uses
+// 9 * 69043). Two carriers become two fp16 weights with two v_perm_b32.
+constexpr uint32_t kByteDigitScale = 69043u;          // ~2^24 / 243
+constexpr uint32_t kTailDigitScale = 9u * 69043u;     // ~2^24 / 27
+
+__device__ __forceinline__ void byte_digit_carriers(uint32_t p, uint32_t (&d)[5]) {
+    uint32_t t = __umul24(p, kByteDigitScale);
+#pragma unroll
+    for (int i = 4; i >= 0; --i) {
+        t = __umul24(t, 3u);
+        d[i] = t;  // digit i (weight 3^i) in bits 24-25
+    }
+}
+
+// {-s, z, +s} selected by digit d: selector bytes (2d, 2d+1) per fp16, from a
+// pair of carriers' top bytes. z is 0, or NaN when the scale is inf/NaN, so that
+// (t - 1) * s keeps IEEE semantics (0 * inf = NaN) exactly.
+__device__ __forceinline__ uint32_t weight_pair(uint32_t even, uint32_t odd, uint32_t table_hi, uint32_t table_lo) {
+    const uint32_t pair = __builtin_amdgcn_perm(odd, even, 0x0c070c03u);  // top bytes -> bytes 0 and 2
+    return __builtin_amdgcn_perm(table_hi, table_lo, __umul24(pair, 0x0202u) + 0x01000100u);
+}
+
+__device__ __forceinline__ void scale_tables(uint32_t s, uint32_t &table_hi, uint32_t &table_lo) {
+    const uint32_t zero = (s & 0x7c00u) == 0x7c00u ? 0x7e00u : 0u;
+    table_lo = (zero << 16) | (s ^ 0x8000u);  // bytes 0-1: -s, bytes 2-3: z
+    table_hi = s;                             // bytes 4-5: +s
+}
+
+// Decodes weights k = 64H .. 64H+63 of one block, in k order, into 32 dwords
+// = 64 fp16 (t - 1) * scale values.
 template <int H>
 __device__ __forceinline__ void decode_half_block(const uint32_t (&w)[kBlockWords], uint32_t (&out)[32]) {
-    const uint32_t s = w[0] & 0xffffu;
-    const uint32_t zero = (s & 0x7c00u) == 0x7c00u ? 0x7e00u : 0u;
-    const uint32_t table_lo = (zero << 16) | (s ^ 0x8000u);  // bytes 0-1: -s, bytes 2-3: z
-    const uint32_t table_hi = s;                             // bytes 4-5: +s
-    // Slots touched by this half: [first_slot, last_slot].
-    constexpr int first_slot = H == 0 ? 0 : 12;
-    constexpr int last_slot = H == 0 ? 12 : kFullSlots;  // slot 25 is the tail byte
-    uint32_t digit[(last_slot - first_slot + 1) * 5];
+    uint32_t table_hi, table_lo;
+    scale_tables(w[0] & 0xffffu, table_hi, table_lo);
+    // Code bytes touched by this half: [first, last]; slot 25 is the tail byte.
+    constexpr int first = H == 0 ? 0 : 12;
+    constexpr int last = H == 0 ? 12 : kFullSlots;
+    uint32_t c[(last - first + 1) * 5];
 #pragma unroll
-    for (int sl = first_slot; sl <= last_slot; ++sl) {
-        uint32_t q = block_byte(w, 2 + sl);
+    for (int sl = first; sl <= last; ++sl) {
+        const uint32_t p = block_byte(w, 2 + sl);
+        uint32_t d[5];
+        if (sl < kFullSlots) {
+            byte_digit_carriers(p, d);
+        } else {
+            uint32_t t = __umul24(p, kTailDigitScale);
 #pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const uint32_t q3 = (q * 171u) >> 9;
-            digit[(sl - first_slot) * 5 + i] = q - 3u * q3;
-            q = q3;
+            for (int i = 2; i >= 0; --i) {
+                t = __umul24(t, 3u);
+                d[i] = t;
+            }
+            d[3] = d[4] = 0u;
         }
+#pragma unroll
+        for (int i = 0; i < 5; ++i) c[(sl - first) * 5 + i] = d[i];
     }
 #pragma unroll
     for (int p = 0; p < 32; ++p) {
@@ -604,10 +631,9 @@ __device__ __forceinline__ void decode_half_block(const uint32_t (&w)[kBlockWord
             const int k = H * 64 + 2 * p + e;
             const int sl = k < 125 ? k / 5 : kFullSlots;
             const int i = k < 125 ? k % 5 : k - 125;
-            d2[e] = digit[(sl - first_slot) * 5 + i];
+            d2[e] = c[(sl - first) * 5 + i];
         }
-        const uint32_t pair = d2[0] | (d2[1] << 16);  // < 2^24: digits are 0..2 for legal bytes, < 4 always
-        out[p] = __builtin_amdgcn_perm(table_hi, table_lo, __umul24(pair, 0x0202u) + 0x01000100u);
+        out[p] = weight_pair(d2[0], d2[1], table_hi, table_lo);
     }
 }
 
@@ -763,22 +789,6 @@ constexpr int kDirectThreads = kDirectWaves * 64;
 constexpr int kDirectRows = kDirectWaves * 32;          // weight rows per workgroup
 constexpr int kDirectLdsBytes = 160 * 1024 - 1024;      // dynamic LDS budget (gfx950: 160 KiB per workgroup)
 constexpr int kDirectStride = kBlockWeights + 8;      // halves per staged activation row
-constexpr uint32_t kByteDigitScale = 69043u;          // ~2^24 / 243
-constexpr uint32_t kTailDigitScale = 9u * 69043u;     // ~2^24 / 27
-
-__device__ __forceinline__ void byte_digit_carriers(uint32_t p, uint32_t (&d)[5]) {
-    uint32_t t = __umul24(p, kByteDigitScale);
-#pragma unroll
-    for (int i = 4; i >= 0; --i) {
-        t = __umul24(t, 3u);
-        d[i] = t;  // digit i (weight 3^i) in bits 24-25
-    }
-}
-
-__device__ __forceinline__ uint32_t weight_pair(uint32_t even, uint32_t odd, uint32_t table_hi, uint32_t table_lo) {
-    const uint32_t pair = __builtin_amdgcn_perm(odd, even, 0x0c070c03u);  // top bytes -> bytes 0 and 2
-    return __builtin_amdgcn_perm(table_hi, table_lo, __umul24(pair, 0x0202u) + 0x01000100u);
-}
 
 
 // One pipeline step of direct_gemm_kernel: the MFMAs of the current group
@@ -791,10 +801,8 @@ __device__ __forceinline__ void direct_step(float16v (&acc)[NB], const uint32_t 
                                             const uint32_t (&u)[4], uint32_t other, bool upper,
                                             const _Float16 *xb, uint32_t scale_mask = 0xffffu) {
     // scale_mask 0 turns a padding group's weights into +-0.
-    const uint32_t s = (upper ? other : u[0]) & scale_mask;
-    const uint32_t zero = (s & 0x7c00u) == 0x7c00u ? 0x7e00u : 0u;
-    const uint32_t table_lo = (zero << 16) | (s ^ 0x8000u);
-    const uint32_t table_hi = s;
+    uint32_t table_hi, table_lo;
+    scale_tables((upper ? other : u[0]) & scale_mask, table_hi, table_lo);
     uint32_t c[64];
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
