@@ -118,14 +118,19 @@ size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t column
 
 /*
  * MFMA product y = x @ W^T, fp16 activations, v_mfma_f32_32x32x16_f16 with fp32
- * accumulation, in one of two forms (the reference's GemmConfig forms,
+ * accumulation, in one of three forms (the reference's GemmConfig forms,
  * src/ternel_mlx/kernels.py:1043-1188, re-chosen for CDNA4):
  *   TERNEL_TQ1_GEMM_TILE   (prefill) 128x128 output tiles, weights decoded to
  *                          fp16 (t-1)*scale tiles in LDS; x 16-byte aligned;
  *   TERNEL_TQ1_GEMM_DIRECT (M <= 64) weights decoded straight into MFMA
  *                          operand registers, activations staged in LDS,
  *                          split-K reduced in the same launch in chunk order;
- *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 64, TILE above.
+ *   TERNEL_TQ1_GEMM_WIDE   (prefill) weights decoded into operand registers of
+ *                          8 waves of 32 rows, 256 x 256 output tiles, both
+ *                          operands DMA'd to LDS, K split stream-K over one
+ *                          workgroup per CU with an ordered in-launch
+ *                          reduction (k_split must be 0/1; columns < 2^22);
+ *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 64, WIDE above (TILE if k_split > 1).
  * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. k_split divides
  * columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
  * same 64 KiB counter region + fp32 partials contract as ternel_tq1_matmul.
@@ -133,6 +138,7 @@ size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t column
 #define TERNEL_TQ1_GEMM_AUTO 0
 #define TERNEL_TQ1_GEMM_TILE 1
 #define TERNEL_TQ1_GEMM_DIRECT 2
+#define TERNEL_TQ1_GEMM_WIDE 3
 int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
                     int64_t columns, int dtype, int form, int k_split, void *ws, size_t ws_bytes,
                     void *stream);

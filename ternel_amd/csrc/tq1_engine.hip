@@ -879,7 +879,7 @@ __global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
     const bool upper = lane >= 32;
     const int row0 = blockIdx.x * kDirectRows + wave * 32;
     const int g_begin = blockIdx.y * chunk_groups;
@@ -1030,6 +1030,406 @@ __global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
             for (int e = 0; e < 4; ++e)
                 if (n + e < N) yrow[n + e] = static_cast<_Float16>(acc[nb][4 * q + e]);
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// wide_gemm_kernel: prefill y = x @ W^T (large M), direct fragments at scale.
+//
+// Tile = 256 weight rows x 256 activation rows; a workgroup of 8 waves, two
+// per SIMD, so that the trit decode (VALU) of one wave issues while the other
+// wave's MFMAs run. Wave w owns weight rows 32w .. 32w+31: lane l decodes half
+// l/32 of the block of row l%32 (the direct form's K order) straight into the
+// A operand, and each A operand feeds the 8 MFMAs of the tile's 32-row
+// activation blocks, so a decoded dword serves 8 MFMAs.
+//
+// Both operands reach LDS by DMA through buffer resources (no address VALU in
+// the loop; rows past the end of x or of the packed array read as zero): per
+// group step a 64 KiB activation tile and the tile's 7 KiB of packed words, in
+// two-deep rings. At step u the activations of u+1 and the words of u+2 are
+// issued, the words of u+1 are read and decoded stage by stage between the
+// MFMAs of u (over the A registers each stage has just consumed), and the step
+// ends with vmcnt(0) and a barrier: one step of MFMAs hides the DMA latency.
+//
+// Work is split stream-K: the (tile, group) units, tiles ordered activation
+// block major, are cut into gridDim.x equal contiguous ranges, one per
+// workgroup, so every CU gets the same number of group steps whatever the
+// tile count. A tile a workgroup covers completely is written directly; a
+// boundary segment is stored as an fp32 partial (slot 0 = the workgroup's
+// first segment, slot 1 = its last), and the last contributor to arrive adds
+// the tile's partials in workgroup order (deterministic) and writes it.
+// ---------------------------------------------------------------------------
+constexpr int kWideWaves = 8;
+constexpr int kWideThreads = kWideWaves * 64;
+constexpr int kWideRows = kWideWaves * 32;                 // weight rows per tile
+constexpr int kWideBlocks = 8;                             // 32-row activation blocks per tile
+constexpr int kWideCols = kWideBlocks * 32;                // activation rows per tile
+constexpr int kWideRowBlocks = kWideRows / kTileRows;      // 64-row packed blocks per tile
+constexpr int kWideXBytes = kWideCols * kBlockWeights * 2; // one group of a tile's activations
+constexpr int kWideWBytes = kWideRowBlocks * kTileGroupWords * 4;  // one group of a tile's words
+constexpr size_t kWideLdsBytes = 2 * (kWideXBytes + kWideWBytes);
+constexpr int kWideFragFloats = kWideBlocks * 16 * 64;     // one wave's accumulators
+constexpr int kBufferRsrcFlags = 0x00020000;               // gfx9 raw buffer: 32-bit data format
+
+__device__ __forceinline__ int direct_target_unit(int u) { return u < 15 ? u : (u < 30 ? u + 1 : (u == 30 ? 15 : 31)); }
+
+struct WideGeometry {
+    int M, N, G;
+    int row_blocks;  // ceil(N / 64)
+    int tiles_n;     // weight row blocks of 256
+    int tiles;       // tiles_n * ceil(M / 256)
+    int units;       // tiles * G
+    int vector_rows; // y rows start 16-byte aligned (y aligned, N % 8 == 0)
+};
+
+// Units are counted in 32 bits: at most 16384 tiles x 32768 groups.
+__device__ __forceinline__ int wide_unit_begin(int units, int p, int P) {
+    return static_cast<int>(static_cast<int64_t>(units) * p / P);
+}
+__device__ __forceinline__ int wide_owner(int units, int u, int P) {
+    return static_cast<int>((static_cast<int64_t>(u + 1) * P - 1) / units);
+}
+
+// Activations in the direct forms' K order: within every group, 4-half unit u
+// of the copy is unit direct_source_unit(u) of x, so that the wide kernel can
+// stage 16-byte runs with LDS-DMA.
+__global__ __launch_bounds__(kThreads) void permute_activations_kernel(const uint2 *__restrict__ x,
+                                                                      uint2 *__restrict__ xp, int64_t units) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= units) return;
+    xp[i] = x[(i & ~int64_t(31)) + direct_source_unit(static_cast<int>(i & 31))];
+}
+
+// Uses every decoded dword in an empty asm statement, so the decode of a
+// group stays in the step that computes it (else it is sunk past the step's
+// barrier toward the next step's MFMAs).
+__device__ __forceinline__ void pin_decoded(const uint32_t (&a)[32]) {
+#pragma unroll
+    for (int q = 0; q < 32; ++q) asm volatile("" ::"v"(a[q]));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
+    const uint32_t *__restrict__ packed, const _Float16 *__restrict__ xp, _Float16 *__restrict__ y,
+    float *__restrict__ partial, unsigned *__restrict__ counters, WideGeometry geo) {
+    // LDS: activation buffers 0 and 1, then word buffers 0 and 1. Activation
+    // rows are 256 bytes; 16-byte chunk c of row r is stored at chunk
+    // c ^ (r & 15), so the sixteen rows one cycle of a 16-byte-per-lane read
+    // serves (64 banks) hit distinct banks. Word buffer: word j of row r of
+    // 64-row block b at byte b * 1792 + j * 256 + r * 4 (the packed layout).
+    extern __shared__ __attribute__((aligned(16))) unsigned char wide_lds[];
+    __shared__ unsigned s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
+    const bool upper = lane >= 32;
+    const int P = gridDim.x;
+    const int p = blockIdx.x;
+    const int G = geo.G;
+    const int row_bytes = G * kBlockWeights * 2;  // one activation row
+    const int u_begin = wide_unit_begin(geo.units, p, P);
+    const int u_end = wide_unit_begin(geo.units, p + 1, P);
+    if (u_begin >= u_end) return;
+    const int last_u = u_end - 1;
+
+    auto tile_of = [&](int u) { return u / G; };
+    // Position of a unit: weight row tile tn, activation tile tm, group g
+    // (advanced by one unit at a time, so no division runs in the loop).
+    struct Cursor {
+        int tn, tm, g;
+    };
+    auto cursor_of = [&](int u) {
+        const int t = tile_of(u);
+        return Cursor{t % geo.tiles_n, t / geo.tiles_n, u - t * G};
+    };
+    auto advance = [&](Cursor &c, int by) {  // by is 0 or 1; selects, no branches
+        const int g1 = c.g + by;
+        const int wrap = g1 == G;
+        c.g = wrap ? 0 : g1;
+        const int tn1 = c.tn + wrap;
+        const int wrap2 = tn1 == geo.tiles_n;
+        c.tn = wrap2 ? 0 : tn1;
+        c.tm += wrap2;
+    };
+
+    unsigned char *const xbuf0 = wide_lds;
+    unsigned char *const wbuf0 = wide_lds + 2 * kWideXBytes;
+    // DMA of a group's activation tile: 64 blocks of 1 KiB (4 rows), 8 per
+    // wave; lane l of block b fills row 4b + l/16, stored chunk l%16. Block
+    // 8w + j starts at row 32w + 4j: the lane part of the offset depends on
+    // j % 4 only (row % 16), the rest is uniform.
+    uint32_t voff_x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = 4 * j + (lane >> 4);
+        voff_x[j] = static_cast<uint32_t>(row * row_bytes + (((lane & 15) ^ (row & 15)) * 16));
+    }
+    auto issue_x = [&](const Cursor &c, int buf) {
+        const int m0 = c.tm * kWideCols;
+        const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16 *>(xp) + static_cast<int64_t>(m0) * (row_bytes / 2), 0,
+            min(kWideCols, geo.M - m0) * row_bytes, kBufferRsrcFlags);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(xbuf0 + buf * kWideXBytes + (wave * 8 + j) * 1024),
+                                                     16, voff_x[j & 3],
+                                                     (wave * 32 + (j >> 2) * 16) * row_bytes + c.g * 256, 0, 0);
+    };
+    // DMA of a group's words: 64-row block b = wave / 2, words 0-3 by the even
+    // wave and 4-6 by the odd one (its fourth load repeats word 6).
+    const int rb = wave >> 1;
+    const uint32_t voff_w = static_cast<uint32_t>(rb * G * kTileGroupWords * 4 + lane * 4);
+    auto issue_w = [&](const Cursor &c, int buf) {
+        const int rb0 = c.tn * kWideRowBlocks;
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t *>(packed) + static_cast<int64_t>(rb0) * G * kTileGroupWords, 0,
+            min(kWideRowBlocks, geo.row_blocks - rb0) * G * kTileGroupWords * 4, kBufferRsrcFlags);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int j = min((wave & 1) * 4 + jj, kBlockWords - 1);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rw, (lds_void *)(wbuf0 + buf * kWideWBytes + rb * (kTileGroupWords * 4) + j * 256), 4, voff_w,
+                c.g * (kTileGroupWords * 4) + j * 256, 0, 0);
+        }
+    };
+    // The five words lane l decodes: words 3h .. 3h+3 (h = l / 32) and the
+    // other end word (6 for h = 0, 0 -- the scale -- for h = 1).
+    const int wrow = rb * (kTileGroupWords * 4) + ((wave & 1) * 32 + (lane & 31)) * 4;
+    auto read_words = [&](uint32_t (&w)[5], int buf) {
+        const uint32_t *base = reinterpret_cast<const uint32_t *>(wbuf0 + buf * kWideWBytes + wrow);
+        const int first = upper ? 3 : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = base[(first + j) * kTileRows];
+        w[4] = base[(upper ? 0 : 6) * kTileRows];
+    };
+
+    // B fragment of MFMA step st, activation block nb: row 32 nb + (lane & 31),
+    // logical positions 64h + 8st .. +8, i.e. chunk 8h + st of the row, stored
+    // at chunk (8h ^ (lane & 8)) | (st ^ (lane & 7)).
+    const int frag_row = (lane & 31) * kBlockWeights + (((upper ? 8 : 0) ^ (lane & 8)) * 8);
+    const int frag_l7 = lane & 7;
+
+    float16v acc[kWideBlocks];
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int nb = 0; nb < kWideBlocks; ++nb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[nb][e] = 0.0f;
+    };
+    zero_acc();
+
+    // One group step on a single register buffer `a` (32 dwords): stage st
+    // runs MFMA step st of the current group from dwords 4st..4st+3
+    // (activation buffer buf) and then decodes the same dwords of the next
+    // group's words w over them.
+    auto step = [&](uint32_t (&a)[32], const uint32_t (&w)[5], int buf, bool mfma) {
+        uint32_t th = 0, tl = 0;
+        uint32_t c[64];
+        const _Float16 *xb = reinterpret_cast<const _Float16 *>(xbuf0 + buf * kWideXBytes);
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            // Stages are scheduling regions: the decode of a stage is not
+            // hoisted into earlier ones (its carriers would all be live at
+            // once), and the stage's 8 fragment reads can issue up front.
+            __builtin_amdgcn_sched_barrier(0);
+            if (mfma) {
+                half8 af;
+                {
+                    uint4 v = {a[4 * st], a[4 * st + 1], a[4 * st + 2], a[4 * st + 3]};
+                    af = *reinterpret_cast<half8 *>(&v);
+                }
+                half8 bf[kWideBlocks];
+#pragma unroll
+                for (int nb = 0; nb < kWideBlocks; ++nb)
+                    bf[nb] = *reinterpret_cast<const half8 *>(xb + nb * 32 * kBlockWeights + frag_row + ((st ^ frag_l7) * 8));
+#pragma unroll
+                for (int nb = 0; nb < kWideBlocks; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[nb], 0, 0, 0);
+                // the fragment reads first, then each MFMA followed by a
+                // share of the decode
+                __builtin_amdgcn_sched_group_barrier(0x100, kWideBlocks, 0);
+#pragma unroll
+                for (int nb = 0; nb < kWideBlocks; ++nb) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                }
+            }
+            if (st == 0) scale_tables((upper ? w[4] : w[0]) & 0xffffu, th, tl);
+#pragma unroll
+            for (int j = 0; j < 12; ++j) {
+                if ((5 * j) / 8 != st) continue;
+                const int bb = 2 + j;
+                uint32_t d[5];
+                byte_digit_carriers((w[bb >> 2] >> (8 * (bb & 3))) & 0xffu, d);
+#pragma unroll
+                for (int i = 0; i < 5; ++i) c[5 * j + i] = d[i];
+            }
+            if (st == 7) {
+                const uint32_t w6 = upper ? w[3] : w[4];
+                uint32_t d24[5];
+                byte_digit_carriers((w6 >> 16) & 0xffu, d24);
+                uint32_t t = __umul24(w6 >> 24, kTailDigitScale);
+                const uint32_t t2 = t = __umul24(t, 3u);
+                const uint32_t t1 = t = __umul24(t, 3u);
+                const uint32_t t0 = __umul24(t, 3u);
+                c[60] = upper ? d24[4] : d24[0];
+                c[61] = upper ? t0 : d24[1];
+                c[62] = upper ? t1 : d24[2];
+                c[63] = upper ? t2 : d24[3];
+            }
+#pragma unroll
+            for (int q = 4 * st; q < 4 * st + 4; ++q) a[q] = weight_pair(c[2 * q], c[2 * q + 1], th, tl);
+        }
+    };
+
+    // Writes the 16 values of fragment nb of tile t. D[i][j] of a 32x32 tile
+    // sits in lane j + 32 * ((i / 4) % 2), item 4 * (i / 8) + i % 4; i is a
+    // weight row (32 wave + i), j an activation row (32 nb + j). Lanes j and
+    // j + 32 swap half their values (as fp16 pairs) so that each holds two
+    // runs of 8 consecutive rows: two 16-byte stores per lane, not 16 scattered
+    // 2-byte ones. Every lane takes part in the swap; stores are guarded.
+    auto store_frag = [&](int t, int nb, const float *vals) {
+        uint32_t h[4][2];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                h[qq][k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(vals[4 * qq + 2 * k]))) |
+                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(vals[4 * qq + 2 * k + 1]))) << 16);
+        // rows 8qq + 4(lane / 32) + e; the lower lane keeps runs qq = 0, 2, the upper qq = 1, 3
+        uint32_t r[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t send = upper ? h[(k >> 1) * 2][k & 1] : h[(k >> 1) * 2 + 1][k & 1];
+            r[k] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, static_cast<int>(send)));
+        }
+        const int m = (t / geo.tiles_n) * kWideCols + nb * 32 + (lane & 31);
+        if (m >= geo.M) return;
+        _Float16 *yrow = y + static_cast<int64_t>(m) * geo.N;
+#pragma unroll
+        for (int run = 0; run < 2; ++run) {  // rows 16 run + 8 (lane / 32) .. + 8
+            const int n = (t % geo.tiles_n) * kWideRows + wave * 32 + 16 * run + (upper ? 8 : 0);
+            const uint32_t *own = h[2 * run + (upper ? 1 : 0)];
+            uint4 v;
+            if (upper) v = uint4{r[2 * run], r[2 * run + 1], own[0], own[1]};
+            else v = uint4{own[0], own[1], r[2 * run], r[2 * run + 1]};
+            if (geo.vector_rows && n + 8 <= geo.N) {
+                *reinterpret_cast<uint4 *>(yrow + n) = v;
+            } else {
+                const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (n + e < geo.N)
+                        yrow[n + e] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(d[e >> 1] >> (16 * (e & 1))));
+            }
+        }
+    };
+    // Emits tile t, whose segment here is [seg_begin, seg_end): directly if it
+    // is the whole tile, else as a partial; the last contributor to arrive adds
+    // the partials in workgroup order, two fragments at a time.
+    auto emit = [&](int t, int seg_begin, int seg_end) {
+        const int tu0 = t * G, tu1 = tu0 + G;
+        if (seg_begin == tu0 && seg_end == tu1) {
+#pragma unroll
+            for (int nb = 0; nb < kWideBlocks; ++nb) {
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[e] = acc[nb][e];
+                store_frag(t, nb, v);
+            }
+            return;
+        }
+        const int slot = seg_begin == u_begin ? 0 : 1;
+        float *mine = partial + ((static_cast<int64_t>(p) * 2 + slot) * kWideWaves + wave) * kWideFragFloats + lane;
+#pragma unroll
+        for (int nb = 0; nb < kWideBlocks; ++nb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                __hip_atomic_store(mine + (nb * 16 + e) * 64, acc[nb][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vector_memory();
+        __syncthreads();
+        const int q0 = wide_owner(geo.units, tu0, P), q1 = wide_owner(geo.units, tu1 - 1, P);
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     static_cast<unsigned>(q1 - q0);
+        __syncthreads();
+        if (!s_last) return;
+        for (int f0 = 0; f0 < kWideBlocks; f0 += 2) {
+            float sum[2][16];
+            for (int q = q0; q <= q1; ++q) {
+                // The tile is contributor q's first segment unless q starts before it.
+                const int qslot = wide_unit_begin(geo.units, q, P) >= tu0 ? 0 : 1;
+                const float *src = partial + ((static_cast<int64_t>(q) * 2 + qslot) * kWideWaves + wave) * kWideFragFloats + lane;
+                float v[2][16];
+#pragma unroll
+                for (int f = 0; f < 2; ++f)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        v[f][e] = __hip_atomic_load(src + ((f0 + f) * 16 + e) * 64, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int f = 0; f < 2; ++f)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) sum[f][e] = q == q0 ? v[f][e] : sum[f][e] + v[f][e];
+            }
+#pragma unroll
+            for (int f = 0; f < 2; ++f) store_frag(t, f0 + f, sum[f]);
+        }
+        if (tid == 0) __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+
+    // Prefetch cursors: activations one unit ahead, words two; both stop at
+    // the last unit (later prefetches repeat it and are never used).
+    int cx_u = min(u_begin + 1, last_u), cw_u = min(u_begin + 2, last_u);
+    Cursor cx = cursor_of(cx_u), cw = cursor_of(cw_u);
+    uint32_t a[32];
+    {
+        const Cursor c0 = cursor_of(u_begin);
+        const int par = u_begin & 1;
+        issue_x(c0, par);
+        issue_w(c0, par);
+        issue_w(cx, par ^ 1);
+        wait_vector_memory();
+        __syncthreads();
+        uint32_t w[5];
+        read_words(w, par);
+        step(a, w, par, false);  // decode only (0 * inf activations would be NaN)
+        pin_decoded(a);
+        __syncthreads();  // every wave has read the words the first step overwrites
+    }
+
+    // Segments: maximal runs of this workgroup's units within one tile; the
+    // pipeline runs on across them (the decode and prefetches of a segment's
+    // last step already belong to the next one).
+    for (int u = u_begin; u < u_end;) {
+        const int t = tile_of(u);
+        const int seg_begin = u;
+        const int seg_end = min(u_end, (t + 1) * G);
+        zero_acc();
+        for (; u < seg_end; ++u) {
+            const int par = u & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" ::: "memory");
+            issue_x(cx, par ^ 1);
+            issue_w(cw, par);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            const int bx = cx_u < last_u, bw = cw_u < last_u;
+            cx_u += bx;
+            cw_u += bw;
+            advance(cx, bx);
+            advance(cw, bw);
+            uint32_t w[5];
+            read_words(w, par ^ 1);
+            step(a, w, par, true);
+            pin_decoded(a);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vector_memory();
+            asm volatile("s_barrier" ::: "memory");
+        }
+        emit(t, seg_begin, seg_end);
     }
 }
 
@@ -1328,9 +1728,87 @@ int launch_direct(const uint32_t *packed, const void *x, void *y, int64_t M, int
     }
 }
 
-int resolve_gemm_form(int64_t M, int form) {
-    if (form == TERNEL_TQ1_GEMM_AUTO) return M <= kDirectMaxBatch ? TERNEL_TQ1_GEMM_DIRECT : TERNEL_TQ1_GEMM_TILE;
-    return form;
+// Wide form: stream-K over one workgroup per CU. Buffer resources address one
+// activation tile (256 rows) and one weight row tile (4 packed 64-row blocks)
+// with 32-bit byte offsets.
+constexpr int64_t kWideMaxColumns = INT32_MAX / (kWideCols * 2) / kBlockWeights * kBlockWeights;
+int device_cu_count() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 256;
+    return cus;
+}
+
+struct WidePlan {
+    WideGeometry geo;
+    int workgroups;
+    size_t partial_bytes;
+    size_t xp_bytes;
+};
+
+int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *plan) {
+    if (k_split > 1)
+        return fail(TERNEL_TQ1_EINVAL, "the wide form splits K by stream-K; k split must be 0 or 1, got %d", k_split);
+    if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
+    if (columns > kWideMaxColumns)
+        return fail(TERNEL_TQ1_EINVAL, "the wide form takes at most %lld columns, got %lld",
+                    static_cast<long long>(kWideMaxColumns), static_cast<long long>(columns));
+    WideGeometry &g = plan->geo;
+    g.M = static_cast<int>(M);
+    g.N = static_cast<int>(rows);
+    g.G = static_cast<int>(columns / kBlockWeights);
+    g.row_blocks = static_cast<int>(ceil_div(rows, kTileRows));
+    g.tiles_n = static_cast<int>(ceil_div(rows, kWideRows));
+    const int64_t tiles = g.tiles_n * ceil_div(M, kWideCols);
+    if (tiles > kCounterSlots)
+        return fail(TERNEL_TQ1_EINVAL, "%lld output tiles exceed the %d stream-K counters", static_cast<long long>(tiles),
+                    kCounterSlots);
+    g.tiles = static_cast<int>(tiles);
+    g.units = static_cast<int>(tiles * g.G);  // < 2^14 tiles x 2^15 groups
+    g.vector_rows = 0;                         // set at launch from the output pointer
+    int64_t wgs = device_cu_count();
+    if (wgs > g.units) wgs = g.units;
+    plan->workgroups = static_cast<int>(wgs);
+    // two partial slots per workgroup, each all of its waves' accumulators
+    plan->partial_bytes = static_cast<size_t>(wgs) * 2 * kWideWaves * kWideFragFloats * sizeof(float);
+    // the permuted copy of the activations follows the partials
+    plan->xp_bytes = static_cast<size_t>(M) * columns * sizeof(_Float16);
+    return TERNEL_TQ1_OK;
+}
+
+int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &plan, void *ws, hipStream_t stream) {
+    static bool attribute_set = false;  // dynamic LDS above 64 KiB needs the opt-in once
+    if (!attribute_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&wide_gemm_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(kWideLdsBytes));
+        if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attribute_set = true;
+    }
+    unsigned *counters = static_cast<unsigned *>(ws);
+    float *partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes);
+    _Float16 *xp = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kCounterRegionBytes + plan.partial_bytes);
+    const int64_t units = static_cast<int64_t>(plan.geo.M) * plan.geo.G * 32;  // 8-byte units of x
+    hipLaunchKernelGGL(permute_activations_kernel, dim3(static_cast<unsigned>(ceil_div(units, kThreads))),
+                       dim3(kThreads), 0, stream, static_cast<const uint2 *>(x), reinterpret_cast<uint2 *>(xp), units);
+    TQ1_LAUNCH_CHECK();
+    WideGeometry geo = plan.geo;
+    geo.vector_rows = geo.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    hipLaunchKernelGGL(wide_gemm_kernel, dim3(static_cast<unsigned>(plan.workgroups)), dim3(kWideThreads),
+                       kWideLdsBytes, stream, packed, xp, static_cast<_Float16 *>(y), partial, counters, geo);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+// Automatic choice: the direct form up to 64 activation rows, the wide form
+// above (faster than the tile form at every measured prefill shape) unless a
+// fixed K split is asked for or the rows are too long for its 32-bit buffer
+// offsets.
+int resolve_gemm_form(int64_t M, int64_t columns, int form, int k_split) {
+    if (form != TERNEL_TQ1_GEMM_AUTO) return form;
+    if (M <= kDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
+    return k_split <= 1 && columns <= kWideMaxColumns ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_TILE;
 }
 
 // The dispatch rule of packed_matmul, retuned for MI355X: the LUT23 kernel up
@@ -1458,11 +1936,16 @@ int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M,
 
 size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
-    form = resolve_gemm_form(M, form);
+    form = resolve_gemm_form(M, columns, form, k_split);
     if (form == TERNEL_TQ1_GEMM_DIRECT) {
         DirectPlan direct;
         if (plan_direct(M, rows, columns, k_split, &direct) != TERNEL_TQ1_OK) return 0;
         return direct.k_split > 1 ? kCounterRegionBytes + direct.partial_bytes : 0;
+    }
+    if (form == TERNEL_TQ1_GEMM_WIDE) {
+        WidePlan wide;
+        if (plan_wide(M, rows, columns, k_split, &wide) != TERNEL_TQ1_OK) return 0;
+        return kCounterRegionBytes + wide.partial_bytes + wide.xp_bytes;
     }
     if (form != TERNEL_TQ1_GEMM_TILE) return 0;
     GemmPlan plan;
@@ -1478,9 +1961,10 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if (dtype != TERNEL_TQ1_F16)
         return fail(TERNEL_TQ1_EINVAL, "the MFMA path takes fp16 activations, got dtype code %d", dtype);
-    if (form != TERNEL_TQ1_GEMM_AUTO && form != TERNEL_TQ1_GEMM_TILE && form != TERNEL_TQ1_GEMM_DIRECT)
+    if (form != TERNEL_TQ1_GEMM_AUTO && form != TERNEL_TQ1_GEMM_TILE && form != TERNEL_TQ1_GEMM_DIRECT &&
+        form != TERNEL_TQ1_GEMM_WIDE)
         return fail(TERNEL_TQ1_EINVAL, "unknown GEMM form %d", form);
-    form = resolve_gemm_form(M, form);
+    form = resolve_gemm_form(M, columns, form, k_split);
     if (form == TERNEL_TQ1_GEMM_DIRECT) {
         DirectPlan direct;
         if ((rc = plan_direct(M, rows, columns, k_split, &direct)) != TERNEL_TQ1_OK) return rc;
@@ -1492,6 +1976,18 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
             return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
                         need);
         return launch_direct(packed, x, y, M, rows, columns, direct, ws, static_cast<hipStream_t>(stream));
+    }
+    if (form == TERNEL_TQ1_GEMM_WIDE) {
+        WidePlan wide;
+        if ((rc = plan_wide(M, rows, columns, k_split, &wide)) != TERNEL_TQ1_OK) return rc;
+        if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+        if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+        if (reinterpret_cast<uintptr_t>(x) & 15u) return fail(TERNEL_TQ1_EINVAL, "activations must be 16-byte aligned");
+        const size_t need = kCounterRegionBytes + wide.partial_bytes + wide.xp_bytes;
+        if (!ws || ws_bytes < need)
+            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
+                        need);
+        return launch_wide(packed, x, y, wide, ws, static_cast<hipStream_t>(stream));
     }
     GemmPlan plan;
     if ((rc = plan_gemm(M, rows, columns, k_split, &plan)) != TERNEL_TQ1_OK) return rc;

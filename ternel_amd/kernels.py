@@ -57,7 +57,7 @@ class MatmulConfig:
         return name if self.k_split in (0, 1) else f"{name}_k{self.k_split}"
 
 
-GEMM_FORMS = {"auto": 0, "tile": 1, "direct": 2}
+GEMM_FORMS = {"auto": 0, "tile": 1, "direct": 2, "wide": 3}
 DIRECT_MAX_BATCH = 64
 
 
@@ -69,7 +69,10 @@ class GemmConfig:
     reference's ``direct_fragments`` switch (src/ternel_mlx/kernels.py:1043-1188):
     ``"tile"`` decodes 128x128 weight tiles into LDS (prefill), ``"direct"``
     decodes straight into MFMA operand registers (at most 64 activation rows),
-    ``"auto"`` takes ``"direct"`` up to 64 rows and ``"tile"`` above.
+    ``"wide"`` decodes into the operand registers of 256x256 output tiles split
+    stream-K over the CUs (prefill; K split 0 or 1), ``"auto"`` takes
+    ``"direct"`` up to 64 rows and ``"wide"`` above (``"tile"`` when a K split
+    above 1 is fixed).
     """
 
     k_split: int = 0

@@ -25,7 +25,7 @@ NORTH_STAR_TOLERANCE = 1e-3
 FP16_UNIT_ROUNDOFF = 2.0 ** -11
 
 
-FORMS = ("tile", "direct")
+FORMS = ("tile", "direct", "wide")
 
 
 def run(blocks: np.ndarray, x16: np.ndarray, *, k_split: int = 0, form: str = "auto") -> np.ndarray:
@@ -61,7 +61,7 @@ def test_mfma_lane_layout_probe(form: str, offset: int) -> None:
     order of the activations that differs from the weights' moves values to
     other positions, which this catches element by element.
     """
-    rows, columns = 256, 256
+    rows, columns = 256, 512
     blocks = random_blocks(rows, columns, seed=11)
     x = np.zeros((64, columns), dtype=np.float16)
     x[np.arange(64), offset + np.arange(64)] = 1.0
@@ -86,7 +86,7 @@ def test_gemm_matches_the_oracle(form: str, rows: int, columns: int, batch: int)
     assert_fp16_faithful(run(blocks, x, form=form), blocks, x)
 
 
-@pytest.mark.parametrize("form", FORMS)
+@pytest.mark.parametrize("form", ("tile", "direct"))
 @pytest.mark.parametrize("k_split", (1, 2, 5, 8, 40))
 def test_gemm_split_k_matches_the_oracle(form: str, k_split: int) -> None:
     blocks = random_blocks(384, 5120, seed=k_split)
@@ -106,7 +106,7 @@ def test_gemm_split_k_is_exact_on_integer_data(form: str) -> None:
     # Integer results up to 5120 in magnitude are exact in fp16 only below 2048;
     # compare through fp16 rounding of the exact answer.
     want16 = want.astype(np.float16).astype(np.float64)
-    for k in (1, 2, 4, 5, 8, 10, 20, 40):
+    for k in ((1,) if form == "wide" else (1, 2, 4, 5, 8, 10, 20, 40)):
         np.testing.assert_array_equal(run(blocks, x, k_split=k, form=form), want16, err_msg=f"k_split={k}")
 
 
@@ -114,20 +114,22 @@ def test_gemm_split_k_is_exact_on_integer_data(form: str) -> None:
 def test_gemm_is_deterministic(form: str) -> None:
     blocks = random_blocks(512, 5120, seed=5)
     x = np.random.default_rng(5).normal(0, 1, size=(64, 5120)).astype(np.float16)
-    first = run(blocks, x, k_split=8, form=form)
+    split = 0 if form == "wide" else 8
+    first = run(blocks, x, k_split=split, form=form)
     for _ in range(2):
-        np.testing.assert_array_equal(run(blocks, x, k_split=8, form=form), first)
+        np.testing.assert_array_equal(run(blocks, x, k_split=split, form=form), first)
 
 
 @pytest.mark.parametrize("form", FORMS)
 def test_gemm_propagates_non_finite_activations(form: str) -> None:
-    blocks = random_blocks(256, 384, seed=7)
-    x = np.zeros((3, 384), dtype=np.float16)
+    columns = 512
+    blocks = random_blocks(256, columns, seed=7)
+    x = np.zeros((3, columns), dtype=np.float16)
     x[0, 0] = np.nan
     x[1, 125] = np.inf
-    x[2, 383] = -np.inf
+    x[2, columns - 1] = -np.inf
     got = run(blocks, x, form=form)
-    want = O.oracle_matmul(blocks, x.astype(np.float64), rows=256, columns=384)
+    want = O.oracle_matmul(blocks, x.astype(np.float64), rows=256, columns=columns)
     assert O.compare(got, want)["pattern_mismatches"] == 0
 
 
@@ -144,19 +146,33 @@ def test_gemm_rejects_other_dtypes_and_bad_splits() -> None:
     with pytest.raises(FormatError, match="at most 64 activation rows"):
         tq1_gemm(blocks, torch.zeros((65, 384), device="cuda", dtype=torch.float16), layout=lay,
                  config=GemmConfig(form="direct"))
+    with pytest.raises(FormatError, match="stream-K"):
+        tq1_gemm(blocks, torch.zeros((4, 384), device="cuda", dtype=torch.float16), layout=lay,
+                 config=GemmConfig(form="wide", k_split=3))
+
+
+@pytest.mark.parametrize(("rows", "columns", "batch"), ((256, 5120, 5), (512, 17408, 300), (4096, 2048, 129)))
+def test_wide_stream_k_reduces_every_tile(rows: int, columns: int, batch: int) -> None:
+    """Stream-K with many contributors per tile (one 256-row tile of 40 groups
+    spread over 40 workgroups; ragged activation tiles), each reduced in order."""
+    blocks = random_blocks(rows, columns, seed=rows + batch)
+    x = np.random.default_rng(batch).normal(0.0, 0.5, size=(batch, columns)).astype(np.float16)
+    got = run(blocks, x, form="wide")
+    assert_fp16_faithful(got, blocks, x)
+    np.testing.assert_array_equal(run(blocks, x, form="wide"), got)  # deterministic
 
 
 @pytest.mark.parametrize("form", FORMS)
 def test_gemm_non_finite_scales_follow_ieee(form: str) -> None:
     """A zero trit times an inf/NaN scale is NaN, as (t - 1) * scale computes it."""
-    rows, columns = 128, 256
+    rows, columns = 128, 512
     rng = np.random.default_rng(9)
-    scale_values = np.full(rows * 2, 0.5, dtype=np.float16)
+    scale_values = np.full(rows * 4, 0.5, dtype=np.float16)
     scale_values[3] = np.inf
     scale_values[64] = -np.inf
     scale_values[130] = np.nan
-    trits = rng.integers(0, 3, size=(rows * 2, 128), dtype=np.uint8)
-    blocks = O.encode_tq1_blocks(scale_values.view(np.uint8).reshape(-1, 2), trits).reshape(rows, 2, 28)
+    trits = rng.integers(0, 3, size=(rows * 4, 128), dtype=np.uint8)
+    blocks = O.encode_tq1_blocks(scale_values.view(np.uint8).reshape(-1, 2), trits).reshape(rows, 4, 28)
     x = rng.normal(0, 1, size=(4, columns)).astype(np.float16)
     got = run(blocks, x, form=form)
     want = O.oracle_matmul(blocks, x.astype(np.float64), rows=rows, columns=columns)
