@@ -1070,6 +1070,7 @@ constexpr int kWideWBytes = kWideRowBlocks * kTileGroupWords * 4;  // one group 
 constexpr size_t kWideLdsBytes = 2 * (kWideXBytes + kWideWBytes);
 constexpr int kWideFragFloats = kWideBlocks * 16 * 64;     // one wave's accumulators
 constexpr int kBufferRsrcFlags = 0x00020000;               // gfx9 raw buffer: 32-bit data format
+constexpr int kWideTileSlots = 8192;                       // stream-K counter pairs (arrivals, publications)
 
 __device__ __forceinline__ int direct_target_unit(int u) { return u < 15 ? u : (u < 30 ? u + 1 : (u == 30 ? 15 : 31)); }
 
@@ -1109,6 +1110,8 @@ __device__ __forceinline__ void pin_decoded(const uint32_t (&a)[32]) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x4 __attribute__((vector_size(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     const uint32_t *__restrict__ packed, const _Float16 *__restrict__ xp, _Float16 *__restrict__ y,
@@ -1228,11 +1231,25 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         uint32_t th = 0, tl = 0;
         uint32_t c[64];
         const _Float16 *xb = reinterpret_cast<const _Float16 *>(xbuf0 + buf * kWideXBytes);
+        auto frag = [&](int st, int nb) {
+            return *reinterpret_cast<const half8 *>(xb + nb * 32 * kBlockWeights + frag_row + ((st ^ frag_l7) * 8));
+        };
+        // Activation fragments in two sets of four blocks: a set is read for
+        // stage st + 1 as soon as the MFMAs of stage st have consumed it, so
+        // the reads overlap the other set's MFMAs.
+        half8 bx[4], by[4];
+        if (mfma) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                bx[i] = frag(0, i);
+                by[i] = frag(0, 4 + i);
+            }
+        }
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
             // Stages are scheduling regions: the decode of a stage is not
             // hoisted into earlier ones (its carriers would all be live at
-            // once), and the stage's 8 fragment reads can issue up front.
+            // once).
             __builtin_amdgcn_sched_barrier(0);
             if (mfma) {
                 half8 af;
@@ -1240,20 +1257,29 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                     uint4 v = {a[4 * st], a[4 * st + 1], a[4 * st + 2], a[4 * st + 3]};
                     af = *reinterpret_cast<half8 *>(&v);
                 }
-                half8 bf[kWideBlocks];
 #pragma unroll
-                for (int nb = 0; nb < kWideBlocks; ++nb)
-                    bf[nb] = *reinterpret_cast<const half8 *>(xb + nb * 32 * kBlockWeights + frag_row + ((st ^ frag_l7) * 8));
+                for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bx[i], acc[i], 0, 0, 0);
+                if (st < 7) {
 #pragma unroll
-                for (int nb = 0; nb < kWideBlocks; ++nb)
-                    acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[nb], 0, 0, 0);
-                // the fragment reads first, then each MFMA followed by a
-                // share of the decode
-                __builtin_amdgcn_sched_group_barrier(0x100, kWideBlocks, 0);
+                    for (int i = 0; i < 4; ++i) bx[i] = frag(st + 1, i);
+                }
 #pragma unroll
-                for (int nb = 0; nb < kWideBlocks; ++nb) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                for (int i = 0; i < 4; ++i)
+                    acc[4 + i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, by[i], acc[4 + i], 0, 0, 0);
+                if (st < 7) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) by[i] = frag(st + 1, 4 + i);
+                }
+                // each MFMA followed by a share of the decode, the next
+                // stage's reads after the MFMAs of their set
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                    }
+                    if (st < 7) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
                 }
             }
             if (st == 0) scale_tables((upper ? w[4] : w[0]) & 0xffffu, th, tl);
@@ -1326,9 +1352,29 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             }
         }
     };
+    // Stream-K reduction. A tile split over workgroups q0..q1 is summed in
+    // workgroup order by the last of them to arrive (counters[t] counts
+    // arrivals), from its own accumulators and the partials the others stored
+    // (counters[kWideTileSlots + t] counts those published). A workgroup that
+    // is not last stores its partial and publishes it only after the next
+    // step's vmcnt(0) and barrier, so no step waits for the stores; the last
+    // arriver waits for the publications, which never wait on anything.
+    int pending = -1;  // tile of a stored, not yet published partial (uniform)
+    auto publish = [&]() {  // after a vmcnt(0) and a barrier: the stores are complete
+        if (pending >= 0 && tid == 0)
+            __hip_atomic_fetch_add(counters + kWideTileSlots + pending, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pending = -1;
+    };
+    // Partials: per workgroup two slots (0 = its first segment, 1 = its last),
+    // per wave 8 fragments x 4 runs of (64 lanes x 4 floats), device-coherent
+    // 16-byte accesses (sc1).
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc(partial, 0, P * 2 * kWideWaves * kWideFragFloats * 4, kBufferRsrcFlags);
+    const uint32_t voff_p = static_cast<uint32_t>((wave * kWideFragFloats + lane * 4) * 4);
+    constexpr int kDeviceCoherent = 16;  // cache policy SC1
+    auto slot_base = [&](int q, int slot) { return (q * 2 + slot) * kWideWaves * kWideFragFloats * 4; };
     // Emits tile t, whose segment here is [seg_begin, seg_end): directly if it
-    // is the whole tile, else as a partial; the last contributor to arrive adds
-    // the partials in workgroup order, two fragments at a time.
+    // is the whole tile, else through the reduction above.
     auto emit = [&](int t, int seg_begin, int seg_end) {
         const int tu0 = t * G, tu1 = tu0 + G;
         if (seg_begin == tu0 && seg_end == tu1) {
@@ -1341,43 +1387,65 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             }
             return;
         }
-        const int slot = seg_begin == u_begin ? 0 : 1;
-        float *mine = partial + ((static_cast<int64_t>(p) * 2 + slot) * kWideWaves + wave) * kWideFragFloats + lane;
-#pragma unroll
-        for (int nb = 0; nb < kWideBlocks; ++nb)
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                __hip_atomic_store(mine + (nb * 16 + e) * 64, acc[nb][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_vector_memory();
-        __syncthreads();
         const int q0 = wide_owner(geo.units, tu0, P), q1 = wide_owner(geo.units, tu1 - 1, P);
         if (tid == 0)
             s_last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                      static_cast<unsigned>(q1 - q0);
         __syncthreads();
-        if (!s_last) return;
-        for (int f0 = 0; f0 < kWideBlocks; f0 += 2) {
-            float sum[2][16];
-            for (int q = q0; q <= q1; ++q) {
-                // The tile is contributor q's first segment unless q starts before it.
-                const int qslot = wide_unit_begin(geo.units, q, P) >= tu0 ? 0 : 1;
-                const float *src = partial + ((static_cast<int64_t>(q) * 2 + qslot) * kWideWaves + wave) * kWideFragFloats + lane;
-                float v[2][16];
+        if (!s_last) {
+            const int base = slot_base(p, seg_begin == u_begin ? 0 : 1);
 #pragma unroll
-                for (int f = 0; f < 2; ++f)
+            for (int nb = 0; nb < kWideBlocks; ++nb)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        v[f][e] = __hip_atomic_load(src + ((f0 + f) * 16 + e) * 64, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                for (int f = 0; f < 2; ++f)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) sum[f][e] = q == q0 ? v[f][e] : sum[f][e] + v[f][e];
-            }
-#pragma unroll
-            for (int f = 0; f < 2; ++f) store_frag(t, f0 + f, sum[f]);
+                for (int r = 0; r < 4; ++r) {
+                    const f32x4 v = {acc[nb][4 * r], acc[nb][4 * r + 1], acc[nb][4 * r + 2], acc[nb][4 * r + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp, voff_p,
+                                                           base + (nb * 4 + r) * 1024, kDeviceCoherent);
+                }
+            pending = t;
+            return;
         }
-        if (tid == 0) __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Last to arrive: wait (bounded) until the others' partials are published.
+        if (tid == 0) {
+            for (int spin = 0; spin < (1 << 22); ++spin) {
+                if (__hip_atomic_load(counters + kWideTileSlots + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+                    static_cast<unsigned>(q1 - q0))
+                    break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int nb = 0; nb < kWideBlocks; ++nb) {
+            float sum[16];
+            for (int q = q0; q <= q1; ++q) {
+                float v[16];
+                if (q == p) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) v[e] = acc[nb][e];
+                } else {
+                    // The tile is contributor q's first segment unless q starts before it.
+                    const int base = slot_base(q, wide_unit_begin(geo.units, q, P) >= tu0 ? 0 : 1);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const f32x4 f = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, voff_p, base + (nb * 4 + r) * 1024,
+                                                                          kDeviceCoherent));
+                        v[4 * r] = f.x;
+                        v[4 * r + 1] = f.y;
+                        v[4 * r + 2] = f.z;
+                        v[4 * r + 3] = f.w;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e) sum[e] = q == q0 ? v[e] : sum[e] + v[e];
+            }
+            store_frag(t, nb, sum);
+        }
+        if (tid == 0) {
+            __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(counters + kWideTileSlots + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     };
 
     // Prefetch cursors: activations one unit ahead, words two; both stop at
@@ -1428,9 +1496,13 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             __builtin_amdgcn_sched_barrier(0);
             wait_vector_memory();
             asm volatile("s_barrier" ::: "memory");
+            publish();
         }
         emit(t, seg_begin, seg_end);
     }
+    wait_vector_memory();
+    __syncthreads();
+    publish();
 }
 
 // ---------------------------------------------------------------------------
@@ -1761,9 +1833,10 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
     g.row_blocks = static_cast<int>(ceil_div(rows, kTileRows));
     g.tiles_n = static_cast<int>(ceil_div(rows, kWideRows));
     const int64_t tiles = g.tiles_n * ceil_div(M, kWideCols);
-    if (tiles > kCounterSlots)
+    static_assert(2 * kWideTileSlots <= kCounterSlots, "two counters per wide tile");
+    if (tiles > kWideTileSlots)
         return fail(TERNEL_TQ1_EINVAL, "%lld output tiles exceed the %d stream-K counters", static_cast<long long>(tiles),
-                    kCounterSlots);
+                    kWideTileSlots);
     g.tiles = static_cast<int>(tiles);
     g.units = static_cast<int>(tiles * g.G);  // < 2^14 tiles x 2^15 groups
     g.vector_rows = 0;                         // set at launch from the output pointer
