@@ -121,15 +121,23 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def is_engine_kernel(name: str) -> bool:
+    """The library's kernels (anonymous-namespace symbols) and the runtime's copy blit."""
+    return "_GLOBAL__N_" in name or name.startswith("(anonymous namespace)::") or name == "__amd_rocclr_copyBuffer"
+
+
 def trace_summary(path: str) -> int:
-    """Per-(kernel, grid) launch statistics from a rocprofv3 kernel_trace.csv: the
-    kernel statistics file groups every grid of one template instance together."""
+    """Per-(kernel, grid) launch statistics of the engine's kernels from a rocprofv3
+    kernel_trace.csv (the kernel statistics file groups every grid of one template
+    instance together); torch's kernels of the synthetic-data setup are left out."""
     import csv
     import statistics
 
     groups: dict = {}
     with open(path, newline="") as f:
         for row in csv.DictReader(f):
+            if not is_engine_kernel(row["Kernel_Name"]):
+                continue
             key = (row["Kernel_Name"], row["Grid_Size_X"], row["Grid_Size_Y"], row["Grid_Size_Z"])
             groups.setdefault(key, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
     print(f"{'calls':>6} {'avg_us':>9} {'median_us':>9} {'min_us':>8} {'max_us':>8}  grid (x,y,z)  kernel")
