@@ -125,12 +125,14 @@ size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t column
  *   TERNEL_TQ1_GEMM_DIRECT (M <= 64) weights decoded straight into MFMA
  *                          operand registers, activations staged in LDS,
  *                          split-K reduced in the same launch in chunk order;
- *   TERNEL_TQ1_GEMM_WIDE   (prefill) weights decoded into operand registers of
- *                          8 waves of 32 rows, 256 x 256 output tiles, both
- *                          operands DMA'd to LDS, K split stream-K over one
- *                          workgroup per CU with an ordered in-launch
- *                          reduction (k_split must be 0/1; columns < 2^22);
- *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 64, WIDE above (TILE if k_split > 1).
+ *   TERNEL_TQ1_GEMM_WIDE   (M > 32, prefill) weights decoded into operand
+ *                          registers of 8 waves of 32 rows, 256-row output
+ *                          tiles 32, 64, 128 or 256 activation rows wide (the
+ *                          narrowest that holds M), both operands DMA'd to
+ *                          LDS, K split stream-K over one workgroup per CU
+ *                          with an ordered in-launch reduction (k_split must
+ *                          be 0/1; columns < 2^22);
+ *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 32, WIDE above (TILE if k_split > 1).
  * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. k_split divides
  * columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
  * same 64 KiB counter region + fp32 partials contract as ternel_tq1_matmul.

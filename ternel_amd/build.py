@@ -30,6 +30,8 @@ HIPCC_FLAGS = [
     "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # a kernel whose host launch stub was not emitted must fail the build, not the load
+    "-Wl,--no-undefined",
 ]
 
 

@@ -1062,13 +1062,22 @@ __global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
 constexpr int kWideWaves = 8;
 constexpr int kWideThreads = kWideWaves * 64;
 constexpr int kWideRows = kWideWaves * 32;                 // weight rows per tile
-constexpr int kWideBlocks = 8;                             // 32-row activation blocks per tile
-constexpr int kWideCols = kWideBlocks * 32;                // activation rows per tile
+constexpr int kWideMaxBlocks = 8;                          // 32-row activation blocks per tile, at most
+constexpr int kWideMaxCols = kWideMaxBlocks * 32;          // activation rows per tile, at most
 constexpr int kWideRowBlocks = kWideRows / kTileRows;      // 64-row packed blocks per tile
-constexpr int kWideXBytes = kWideCols * kBlockWeights * 2; // one group of a tile's activations
 constexpr int kWideWBytes = kWideRowBlocks * kTileGroupWords * 4;  // one group of a tile's words
-constexpr size_t kWideLdsBytes = 2 * (kWideXBytes + kWideWBytes);
-constexpr int kWideFragFloats = kWideBlocks * 16 * 64;     // one wave's accumulators
+// Per template width NB (32-row activation blocks per tile): one group of a
+// tile's activations, the dynamic LDS, one wave's accumulators.
+constexpr int wide_x_bytes(int nb) { return nb * 32 * kBlockWeights * 2; }
+// DMA ring depth (units): four where 160 KiB of LDS hold it, so that the
+// prefetch distance covers the memory latency when a step is short (narrow
+// tiles; measured on MI355X, two workgroups per CU with shallower rings were
+// slower at M = 8 and 64).
+constexpr int wide_ring(int nb) { return nb >= 8 ? 2 : 4; }
+constexpr size_t wide_lds_bytes(int nb) {
+    return wide_ring(nb) * (static_cast<size_t>(wide_x_bytes(nb)) + kWideWBytes);
+}
+constexpr int wide_frag_floats(int nb) { return nb * 16 * 64; }
 constexpr int kBufferRsrcFlags = 0x00020000;               // gfx9 raw buffer: 32-bit data format
 constexpr int kWideTileSlots = 8192;                       // stream-K counter pairs (arrivals, publications)
 
@@ -1078,7 +1087,7 @@ struct WideGeometry {
     int M, N, G;
     int row_blocks;  // ceil(N / 64)
     int tiles_n;     // weight row blocks of 256
-    int tiles;       // tiles_n * ceil(M / 256)
+    int tiles;       // tiles_n * ceil(M / (32 NB))
     int units;       // tiles * G
     int vector_rows; // y rows start 16-byte aligned (y aligned, N % 8 == 0)
 };
@@ -1113,10 +1122,24 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef uint32_t u32x4 __attribute__((vector_size(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// 16-byte-per-lane LDS-DMA through a buffer resource (gfx950). A plain
+// function, so that its arguments are checked once and not per template
+// instance: the host pass of a kernel template fails to instantiate a direct
+// call whose arguments depend on the template parameter.
+__device__ __forceinline__ void buffer_dma16(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voffset,
+                                             uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)lds, 16, voffset, soffset, 0, 0);
+}
+
+template <int NB>
 __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     const uint32_t *__restrict__ packed, const _Float16 *__restrict__ xp, _Float16 *__restrict__ y,
     float *__restrict__ partial, unsigned *__restrict__ counters, WideGeometry geo) {
-    // LDS: activation buffers 0 and 1, then word buffers 0 and 1. Activation
+    constexpr int kCols = NB * 32;                  // activation rows per tile
+    constexpr int kXBytes = wide_x_bytes(NB);
+    constexpr int kRing = wide_ring(NB);
+    constexpr int kFragFloats = wide_frag_floats(NB);
+    // LDS: a ring of activation buffers, then a ring of word buffers. Activation
     // rows are 256 bytes; 16-byte chunk c of row r is stored at chunk
     // c ^ (r & 15), so the sixteen rows one cycle of a 16-byte-per-lane read
     // serves (64 banks) hit distinct banks. Word buffer: word j of row r of
@@ -1158,27 +1181,28 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     };
 
     unsigned char *const xbuf0 = wide_lds;
-    unsigned char *const wbuf0 = wide_lds + 2 * kWideXBytes;
-    // DMA of a group's activation tile: 64 blocks of 1 KiB (4 rows), 8 per
+    unsigned char *const wbuf0 = wide_lds + kRing * kXBytes;
+    // DMA of a group's activation tile: 8 NB blocks of 1 KiB (4 rows), NB per
     // wave; lane l of block b fills row 4b + l/16, stored chunk l%16. Block
-    // 8w + j starts at row 32w + 4j: the lane part of the offset depends on
-    // j % 4 only (row % 16), the rest is uniform.
-    uint32_t voff_x[4];
+    // b = NB w + j starts at row 4b: the lane part of the offset depends on
+    // b % 4 only (row % 16), the rest (16 (b / 4) rows) is uniform.
+    constexpr int kVoff = NB % 4 == 0 ? 4 : NB;
+    uint32_t voff_x[kVoff];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = 4 * j + (lane >> 4);
+    for (int j = 0; j < kVoff; ++j) {
+        const int row = 4 * ((wave * NB + j) & 3) + (lane >> 4);
         voff_x[j] = static_cast<uint32_t>(row * row_bytes + (((lane & 15) ^ (row & 15)) * 16));
     }
     auto issue_x = [&](const Cursor &c, int buf) {
-        const int m0 = c.tm * kWideCols;
+        const int m0 = c.tm * kCols;
         const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<_Float16 *>(xp) + static_cast<int64_t>(m0) * (row_bytes / 2), 0,
-            min(kWideCols, geo.M - m0) * row_bytes, kBufferRsrcFlags);
+            min(kCols, geo.M - m0) * row_bytes, kBufferRsrcFlags);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(xbuf0 + buf * kWideXBytes + (wave * 8 + j) * 1024),
-                                                     16, voff_x[j & 3],
-                                                     (wave * 32 + (j >> 2) * 16) * row_bytes + c.g * 256, 0, 0);
+        for (int j = 0; j < NB; ++j) {
+            const int b = wave * NB + j;
+            buffer_dma16(rx, xbuf0 + buf * kXBytes + b * 1024, voff_x[j % kVoff], (b >> 2) * 16 * row_bytes + c.g * 256);
+        }
     };
     // DMA of a group's words: 64-row block b = wave / 2, words 0-3 by the even
     // wave and 4-6 by the odd one (its fourth load repeats word 6).
@@ -1214,10 +1238,10 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     const int frag_row = (lane & 31) * kBlockWeights + (((upper ? 8 : 0) ^ (lane & 8)) * 8);
     const int frag_l7 = lane & 7;
 
-    float16v acc[kWideBlocks];
+    float16v acc[NB];
     auto zero_acc = [&]() {
 #pragma unroll
-        for (int nb = 0; nb < kWideBlocks; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[nb][e] = 0.0f;
     };
@@ -1230,15 +1254,16 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     auto step = [&](uint32_t (&a)[32], const uint32_t (&w)[5], int buf, bool mfma) {
         uint32_t th = 0, tl = 0;
         uint32_t c[64];
-        const _Float16 *xb = reinterpret_cast<const _Float16 *>(xbuf0 + buf * kWideXBytes);
+        const _Float16 *xb = reinterpret_cast<const _Float16 *>(xbuf0 + buf * kXBytes);
         auto frag = [&](int st, int nb) {
             return *reinterpret_cast<const half8 *>(xb + nb * 32 * kBlockWeights + frag_row + ((st ^ frag_l7) * 8));
         };
-        // Activation fragments in two sets of four blocks: a set is read for
-        // stage st + 1 as soon as the MFMAs of stage st have consumed it, so
-        // the reads overlap the other set's MFMAs.
+        // Eight blocks: activation fragments in two sets of four, a set read
+        // for stage st + 1 as soon as the MFMAs of stage st have consumed it,
+        // so the reads overlap the other set's MFMAs. Fewer blocks: a stage's
+        // fragments are read at its start.
         half8 bx[4], by[4];
-        if (mfma) {
+        if (NB == 8 && mfma) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 bx[i] = frag(0, i);
@@ -1251,21 +1276,42 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             // hoisted into earlier ones (its carriers would all be live at
             // once).
             __builtin_amdgcn_sched_barrier(0);
-            if (mfma) {
+            if (NB < 8 && mfma) {
+                half8 af;
+                {
+                    uint4 v = {a[4 * st], a[4 * st + 1], a[4 * st + 2], a[4 * st + 3]};
+                    af = *reinterpret_cast<half8 *>(&v);
+                }
+                half8 bf[NB];
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) bf[nb] = frag(st, nb);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[nb], acc[nb], 0, 0, 0);
+                // the fragment reads first, then each MFMA with a share of the decode
+                __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 24 / NB, 0);
+                }
+            }
+            if (NB == 8 && mfma) {
                 half8 af;
                 {
                     uint4 v = {a[4 * st], a[4 * st + 1], a[4 * st + 2], a[4 * st + 3]};
                     af = *reinterpret_cast<half8 *>(&v);
                 }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bx[i], acc[i], 0, 0, 0);
+                for (int i = 0; i < 4; ++i)
+                    acc[i % NB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bx[i], acc[i % NB], 0, 0, 0);
                 if (st < 7) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) bx[i] = frag(st + 1, i);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[4 + i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, by[i], acc[4 + i], 0, 0, 0);
+                    acc[(4 + i) % NB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, by[i], acc[(4 + i) % NB], 0, 0, 0);
                 if (st < 7) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) by[i] = frag(st + 1, 4 + i);
@@ -1331,7 +1377,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             const uint32_t send = upper ? h[(k >> 1) * 2][k & 1] : h[(k >> 1) * 2 + 1][k & 1];
             r[k] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, static_cast<int>(send)));
         }
-        const int m = (t / geo.tiles_n) * kWideCols + nb * 32 + (lane & 31);
+        const int m = (t / geo.tiles_n) * kCols + nb * 32 + (lane & 31);
         if (m >= geo.M) return;
         _Float16 *yrow = y + static_cast<int64_t>(m) * geo.N;
 #pragma unroll
@@ -1366,20 +1412,20 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         pending = -1;
     };
     // Partials: per workgroup two slots (0 = its first segment, 1 = its last),
-    // per wave 8 fragments x 4 runs of (64 lanes x 4 floats), device-coherent
+    // per wave NB fragments x 4 runs of (64 lanes x 4 floats), device-coherent
     // 16-byte accesses (sc1).
     const __amdgpu_buffer_rsrc_t rp =
-        __builtin_amdgcn_make_buffer_rsrc(partial, 0, P * 2 * kWideWaves * kWideFragFloats * 4, kBufferRsrcFlags);
-    const uint32_t voff_p = static_cast<uint32_t>((wave * kWideFragFloats + lane * 4) * 4);
+        __builtin_amdgcn_make_buffer_rsrc(partial, 0, P * 2 * kWideWaves * kFragFloats * 4, kBufferRsrcFlags);
+    const uint32_t voff_p = static_cast<uint32_t>((wave * kFragFloats + lane * 4) * 4);
     constexpr int kDeviceCoherent = 16;  // cache policy SC1
-    auto slot_base = [&](int q, int slot) { return (q * 2 + slot) * kWideWaves * kWideFragFloats * 4; };
+    auto slot_base = [&](int q, int slot) { return (q * 2 + slot) * kWideWaves * kFragFloats * 4; };
     // Emits tile t, whose segment here is [seg_begin, seg_end): directly if it
     // is the whole tile, else through the reduction above.
     auto emit = [&](int t, int seg_begin, int seg_end) {
         const int tu0 = t * G, tu1 = tu0 + G;
         if (seg_begin == tu0 && seg_end == tu1) {
 #pragma unroll
-            for (int nb = 0; nb < kWideBlocks; ++nb) {
+            for (int nb = 0; nb < NB; ++nb) {
                 float v[16];
 #pragma unroll
                 for (int e = 0; e < 16; ++e) v[e] = acc[nb][e];
@@ -1395,7 +1441,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         if (!s_last) {
             const int base = slot_base(p, seg_begin == u_begin ? 0 : 1);
 #pragma unroll
-            for (int nb = 0; nb < kWideBlocks; ++nb)
+            for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const f32x4 v = {acc[nb][4 * r], acc[nb][4 * r + 1], acc[nb][4 * r + 2], acc[nb][4 * r + 3]};
@@ -1416,7 +1462,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         }
         __syncthreads();
 #pragma unroll
-        for (int nb = 0; nb < kWideBlocks; ++nb) {
+        for (int nb = 0; nb < NB; ++nb) {
             float sum[16];
             for (int q = q0; q <= q1; ++q) {
                 float v[16];
@@ -1448,26 +1494,45 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         }
     };
 
-    // Prefetch cursors: activations one unit ahead, words two; both stop at
-    // the last unit (later prefetches repeat it and are never used).
-    int cx_u = min(u_begin + 1, last_u), cw_u = min(u_begin + 2, last_u);
+    // Prefetch cursors: activations kRing - 1 units ahead, words kRing; no
+    // DMA is issued past the last unit (uniform branches). Ring slot of unit
+    // v: v % kRing.
+    int cx_u = u_begin, cw_u = u_begin;
     Cursor cx = cursor_of(cx_u), cw = cursor_of(cw_u);
+    auto next_x = [&]() {
+        ++cx_u;
+        advance(cx, 1);
+    };
+    auto next_w = [&]() {
+        ++cw_u;
+        advance(cw, 1);
+    };
     uint32_t a[32];
     {
-        const Cursor c0 = cursor_of(u_begin);
-        const int par = u_begin & 1;
-        issue_x(c0, par);
-        issue_w(c0, par);
-        issue_w(cx, par ^ 1);
+        for (int v = 0; v < kRing - 1; ++v) {
+            if (cx_u <= last_u) issue_x(cx, (u_begin + v) & (kRing - 1));
+            next_x();
+        }
+        for (int v = 0; v < kRing; ++v) {
+            if (cw_u <= last_u) issue_w(cw, (u_begin + v) & (kRing - 1));
+            next_w();
+        }
         wait_vector_memory();
         __syncthreads();
         uint32_t w[5];
-        read_words(w, par);
-        step(a, w, par, false);  // decode only (0 * inf activations would be NaN)
+        read_words(w, u_begin & (kRing - 1));
+        step(a, w, u_begin & (kRing - 1), false);  // decode only (0 * inf activations would be NaN)
         pin_decoded(a);
         __syncthreads();  // every wave has read the words the first step overwrites
     }
 
+    // s_waitcnt vmcnt(n): at the end of step u the activations of u+1 and the
+    // words of u+2 -- issued kRing - 2 steps earlier, or before the loop --
+    // must have landed; the DMAs of the kRing - 2 later steps may stay in
+    // flight (gfx9 encoding: vmcnt bits 3:0 and 15:14, other counters idle).
+    constexpr int kInFlight = (kRing - 2) * (NB + 4);
+    constexpr unsigned kWaitRing = (kInFlight & 15) | ((kInFlight >> 4) << 14) | 0x0f70;
+    static_assert(kInFlight <= 63, "vmcnt holds at most 63");
     // Segments: maximal runs of this workgroup's units within one tile; the
     // pipeline runs on across them (the decode and prefetches of a segment's
     // last step already belong to the next one).
@@ -1477,24 +1542,25 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         const int seg_end = min(u_end, (t + 1) * G);
         zero_acc();
         for (; u < seg_end; ++u) {
-            const int par = u & 1;
+            const int slot = u & (kRing - 1);
             __builtin_amdgcn_sched_barrier(0);
             asm volatile("" ::: "memory");
-            issue_x(cx, par ^ 1);
-            issue_w(cw, par);
+            if (cx_u <= last_u) issue_x(cx, (slot + kRing - 1) & (kRing - 1));
+            if (cw_u <= last_u) issue_w(cw, slot);
             asm volatile("" ::: "memory");
             __builtin_amdgcn_sched_barrier(0);
-            const int bx = cx_u < last_u, bw = cw_u < last_u;
-            cx_u += bx;
-            cw_u += bw;
-            advance(cx, bx);
-            advance(cw, bw);
+            next_x();
+            next_w();
             uint32_t w[5];
-            read_words(w, par ^ 1);
-            step(a, w, par, true);
+            read_words(w, (slot + 1) & (kRing - 1));
+            step(a, w, slot, true);
             pin_decoded(a);
             __builtin_amdgcn_sched_barrier(0);
-            wait_vector_memory();
+            // A partial stored after the previous step is published once
+            // every store of this workgroup is complete; near the end of the
+            // range fewer DMAs are in flight than the counted wait assumes.
+            if (kRing == 2 || pending >= 0 || u + kRing - 1 > last_u) wait_vector_memory();
+            else __builtin_amdgcn_s_waitcnt(kWaitRing);
             asm volatile("s_barrier" ::: "memory");
             publish();
         }
@@ -1504,6 +1570,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     __syncthreads();
     publish();
 }
+
 
 // ---------------------------------------------------------------------------
 // Host-side geometry
@@ -1801,9 +1868,13 @@ int launch_direct(const uint32_t *packed, const void *x, void *y, int64_t M, int
 }
 
 // Wide form: stream-K over one workgroup per CU. Buffer resources address one
-// activation tile (256 rows) and one weight row tile (4 packed 64-row blocks)
-// with 32-bit byte offsets.
-constexpr int64_t kWideMaxColumns = INT32_MAX / (kWideCols * 2) / kBlockWeights * kBlockWeights;
+// activation tile (up to 256 rows) and one weight row tile (4 packed 64-row
+// blocks) with 32-bit byte offsets.
+constexpr int64_t kWideMaxColumns = INT32_MAX / (kWideMaxCols * 2) / kBlockWeights * kBlockWeights;
+
+// Tile width (32-row activation blocks): the narrowest of 1, 2, 4, 8 that holds
+// the batch, so small batches do not compute empty columns.
+int wide_blocks(int64_t M) { return M <= 32 ? 1 : (M <= 64 ? 2 : (M <= 128 ? 4 : 8)); }
 int device_cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1814,6 +1885,7 @@ int device_cu_count() {
 
 struct WidePlan {
     WideGeometry geo;
+    int nb;  // tile width in 32-row activation blocks
     int workgroups;
     size_t partial_bytes;
     size_t xp_bytes;
@@ -1832,7 +1904,8 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
     g.G = static_cast<int>(columns / kBlockWeights);
     g.row_blocks = static_cast<int>(ceil_div(rows, kTileRows));
     g.tiles_n = static_cast<int>(ceil_div(rows, kWideRows));
-    const int64_t tiles = g.tiles_n * ceil_div(M, kWideCols);
+    plan->nb = wide_blocks(M);
+    const int64_t tiles = g.tiles_n * ceil_div(M, 32 * plan->nb);
     static_assert(2 * kWideTileSlots <= kCounterSlots, "two counters per wide tile");
     if (tiles > kWideTileSlots)
         return fail(TERNEL_TQ1_EINVAL, "%lld output tiles exceed the %d stream-K counters", static_cast<long long>(tiles),
@@ -1844,21 +1917,30 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
     if (wgs > g.units) wgs = g.units;
     plan->workgroups = static_cast<int>(wgs);
     // two partial slots per workgroup, each all of its waves' accumulators
-    plan->partial_bytes = static_cast<size_t>(wgs) * 2 * kWideWaves * kWideFragFloats * sizeof(float);
+    plan->partial_bytes = static_cast<size_t>(wgs) * 2 * kWideWaves * wide_frag_floats(plan->nb) * sizeof(float);
     // the permuted copy of the activations follows the partials
     plan->xp_bytes = static_cast<size_t>(M) * columns * sizeof(_Float16);
     return TERNEL_TQ1_OK;
 }
 
-int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &plan, void *ws, hipStream_t stream) {
+template <int NB>
+int launch_wide_kernel(const uint32_t *packed, const _Float16 *xp, void *y, float *partial, unsigned *counters,
+                       const WideGeometry &geo, int workgroups, hipStream_t stream) {
     static bool attribute_set = false;  // dynamic LDS above 64 KiB needs the opt-in once
     if (!attribute_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&wide_gemm_kernel),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&wide_gemm_kernel<NB>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 static_cast<int>(kWideLdsBytes));
+                                                 static_cast<int>(wide_lds_bytes(NB)));
         if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
         attribute_set = true;
     }
+    hipLaunchKernelGGL(wide_gemm_kernel<NB>, dim3(static_cast<unsigned>(workgroups)), dim3(kWideThreads),
+                       wide_lds_bytes(NB), stream, packed, xp, static_cast<_Float16 *>(y), partial, counters, geo);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &plan, void *ws, hipStream_t stream) {
     unsigned *counters = static_cast<unsigned *>(ws);
     float *partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes);
     _Float16 *xp = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kCounterRegionBytes + plan.partial_bytes);
@@ -1868,19 +1950,27 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
     TQ1_LAUNCH_CHECK();
     WideGeometry geo = plan.geo;
     geo.vector_rows = geo.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
-    hipLaunchKernelGGL(wide_gemm_kernel, dim3(static_cast<unsigned>(plan.workgroups)), dim3(kWideThreads),
-                       kWideLdsBytes, stream, packed, xp, static_cast<_Float16 *>(y), partial, counters, geo);
-    TQ1_LAUNCH_CHECK();
-    return TERNEL_TQ1_OK;
+    switch (plan.nb) {
+        case 1:
+            return launch_wide_kernel<1>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
+        case 2:
+            return launch_wide_kernel<2>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
+        case 4:
+            return launch_wide_kernel<4>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
+        default:
+            return launch_wide_kernel<8>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
+    }
 }
 
-// Automatic choice: the direct form up to 64 activation rows, the wide form
-// above (faster than the tile form at every measured prefill shape) unless a
-// fixed K split is asked for or the rows are too long for its 32-bit buffer
-// offsets.
+// Automatic choice (measured on MI355X over the 27B shapes): the direct form
+// up to 32 activation rows, the wide form above -- 64-row tiles beat the
+// direct form at M = 64 (gate/up 37.6 us against 53.2) and the wide form
+// beats the tile form at every prefill shape -- unless a fixed K split is
+// asked for or the rows are too long for its 32-bit buffer offsets.
+constexpr int64_t kAutoDirectMaxBatch = 32;
 int resolve_gemm_form(int64_t M, int64_t columns, int form, int k_split) {
     if (form != TERNEL_TQ1_GEMM_AUTO) return form;
-    if (M <= kDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
+    if (M <= kAutoDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
     return k_split <= 1 && columns <= kWideMaxColumns ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_TILE;
 }
 

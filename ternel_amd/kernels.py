@@ -69,10 +69,10 @@ class GemmConfig:
     reference's ``direct_fragments`` switch (src/ternel_mlx/kernels.py:1043-1188):
     ``"tile"`` decodes 128x128 weight tiles into LDS (prefill), ``"direct"``
     decodes straight into MFMA operand registers (at most 64 activation rows),
-    ``"wide"`` decodes into the operand registers of 256x256 output tiles split
-    stream-K over the CUs (prefill; K split 0 or 1), ``"auto"`` takes
-    ``"direct"`` up to 64 rows and ``"wide"`` above (``"tile"`` when a K split
-    above 1 is fixed).
+    ``"wide"`` decodes into the operand registers of 256-row output tiles (32
+    to 256 activation rows wide) split stream-K over the CUs (prefill; K split
+    0 or 1), ``"auto"`` takes ``"direct"`` up to 32 rows and ``"wide"`` above
+    (``"tile"`` when a K split above 1 is fixed).
     """
 
     k_split: int = 0

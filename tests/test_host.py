@@ -215,13 +215,20 @@ def test_workspace_queries() -> None:
     assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, direct, 5) == counters + 5 * 2 * 128 * 32 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(40, 300, 5120, direct, 4) == counters + 4 * 3 * 128 * 64 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(65, 256, 5120, direct, 1) == 0  # rejected
-    # wide form: two fp32 partial slots of 8 waves x 8 fragments x 16 x 64 per
+    # wide form: two fp32 partial slots of 8 waves x NB fragments x 16 x 64 per
     # workgroup (one per CU, 256 without a GPU, at most one per unit), then
-    # the K-permuted fp16 copy of the activations
-    wide, slot_pair = 3, 2 * 8 * 8 * 16 * 64 * 4
+    # the K-permuted fp16 copy of the activations;
+    # NB = 1, 2, 4, 8 32-row activation blocks per tile for M <= 32, 64, 128, above
+    wide = 3
+    def slot_pair(nb: int) -> int:
+        return 2 * 8 * nb * 16 * 64 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, wide, 0) == (
-        counters + 256 * slot_pair + 512 * 5120 * 2)
-    assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 1) == counters + 5 * slot_pair + 5 * 640 * 2
+        counters + 256 * slot_pair(8) + 512 * 5120 * 2)
+    assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 1) == counters + 5 * slot_pair(1) + 5 * 640 * 2
+    assert handle.ternel_tq1_gemm_workspace_bytes(64, 17408, 5120, wide, 0) == (
+        counters + 256 * slot_pair(2) + 64 * 5120 * 2)
+    assert handle.ternel_tq1_gemm_workspace_bytes(100, 17408, 5120, wide, 0) == (
+        counters + 256 * slot_pair(4) + 100 * 5120 * 2)
     assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 2) == 0  # K is split by stream-K
     assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 1 << 22, wide, 0) == 0  # 32-bit buffer offsets
     assert handle.ternel_tq1_packed_words(300, 640) == 5 * 5 * 7 * 64
