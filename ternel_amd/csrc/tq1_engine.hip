@@ -1873,8 +1873,21 @@ int launch_direct(const uint32_t *packed, const void *x, void *y, int64_t M, int
 constexpr int64_t kWideMaxColumns = INT32_MAX / (kWideMaxCols * 2) / kBlockWeights * kBlockWeights;
 
 // Tile width (32-row activation blocks): the narrowest of 1, 2, 4, 8 that holds
-// the batch, so small batches do not compute empty columns.
-int wide_blocks(int64_t M) { return M <= 32 ? 1 : (M <= 64 ? 2 : (M <= 128 ? 4 : 8)); }
+// the batch, so small batches do not compute empty columns -- but 128-wide
+// rather than 256-wide tiles where the stream-K reduction would weigh on a
+// short loop.  A split tile's last contributor reads the other contributors'
+// partials, about cus/tiles - 1 of them at tile size each, after a loop of
+// tiles*groups/cus steps; 128-wide tiles halve the partial and, with twice the
+// tiles, the contributors.  Take them while (cus/tiles - 1) / (tiles*groups/cus)
+// exceeds 0.1.  Measured on MI355X (TFLOP/s, 256- / 128-wide tiles): down
+// 17408->5120 M=256 375 / 550, M=512 694 / 775, M=768 835 / 841, M=1024
+// 915 / 877; gate/up 5120->17408 M=256 559 / 687, M=512 865 / 824, M=768
+// 928 / 861.
+int wide_blocks(int64_t M, int64_t tiles_n, int64_t groups, int64_t cus) {
+    const int nb = M <= 32 ? 1 : (M <= 64 ? 2 : (M <= 128 ? 4 : 8));
+    const int64_t tiles = tiles_n * ceil_div(M, 256);
+    return nb == 8 && 10 * (cus - tiles) * cus > tiles * tiles * groups ? 4 : nb;
+}
 int device_cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1904,7 +1917,7 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
     g.G = static_cast<int>(columns / kBlockWeights);
     g.row_blocks = static_cast<int>(ceil_div(rows, kTileRows));
     g.tiles_n = static_cast<int>(ceil_div(rows, kWideRows));
-    plan->nb = wide_blocks(M);
+    plan->nb = wide_blocks(M, g.tiles_n, g.G, device_cu_count());
     const int64_t tiles = g.tiles_n * ceil_div(M, 32 * plan->nb);
     static_assert(2 * kWideTileSlots <= kCounterSlots, "two counters per wide tile");
     if (tiles > kWideTileSlots)

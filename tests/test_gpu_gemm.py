@@ -151,10 +151,13 @@ def test_gemm_rejects_other_dtypes_and_bad_splits() -> None:
                  config=GemmConfig(form="wide", k_split=3))
 
 
-@pytest.mark.parametrize(("rows", "columns", "batch"), ((256, 5120, 5), (512, 17408, 300), (4096, 2048, 129)))
+@pytest.mark.parametrize(("rows", "columns", "batch"),
+                         ((256, 5120, 5), (512, 17408, 300), (4096, 2048, 129), (4096, 17408, 800)))
 def test_wide_stream_k_reduces_every_tile(rows: int, columns: int, batch: int) -> None:
     """Stream-K with many contributors per tile (one 256-row tile of 40 groups
-    spread over 40 workgroups; ragged activation tiles), each reduced in order."""
+    spread over 40 workgroups; ragged activation tiles), each reduced in order.
+    The last case has enough tiles (16 x 4 of 136 groups) for 256-wide
+    activation tiles; the others run 32- to 128-wide ones."""
     blocks = random_blocks(rows, columns, seed=rows + batch)
     x = np.random.default_rng(batch).normal(0.0, 0.5, size=(batch, columns)).astype(np.float16)
     got = run(blocks, x, form="wide")

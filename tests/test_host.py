@@ -218,12 +218,24 @@ def test_workspace_queries() -> None:
     # wide form: two fp32 partial slots of 8 waves x NB fragments x 16 x 64 per
     # workgroup (one per CU, 256 without a GPU, at most one per unit), then
     # the K-permuted fp16 copy of the activations;
-    # NB = 1, 2, 4, 8 32-row activation blocks per tile for M <= 32, 64, 128, above
+    # NB = 1, 2, 4, 8 32-row activation blocks per tile for M <= 32, 64, 128, above,
+    # and 4 instead of 8 while, with 256-wide tiles, the partials a tile's last
+    # contributor reads (256/tiles - 1) exceed a tenth of the steps per CU
+    # (tiles x groups / 256)
     wide = 3
     def slot_pair(nb: int) -> int:
         return 2 * 8 * nb * 16 * 64 * 4
+    # gate/up, 68 x 2 tiles, 40 groups: 0.9 partials after 21.25 steps
     assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, wide, 0) == (
         counters + 256 * slot_pair(8) + 512 * 5120 * 2)
+    # gate/up, 68 tiles: 2.8 partials after 10.6 steps
+    assert handle.ternel_tq1_gemm_workspace_bytes(256, 17408, 5120, wide, 0) == (
+        counters + 256 * slot_pair(4) + 256 * 5120 * 2)
+    # down, 20 x 4 tiles, 136 groups: 2.2 partials after 42.5 steps; 20 x 3: 3.3 after 31.9
+    assert handle.ternel_tq1_gemm_workspace_bytes(1024, 5120, 17408, wide, 0) == (
+        counters + 256 * slot_pair(8) + 1024 * 17408 * 2)
+    assert handle.ternel_tq1_gemm_workspace_bytes(768, 5120, 17408, wide, 0) == (
+        counters + 256 * slot_pair(4) + 768 * 17408 * 2)
     assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 1) == counters + 5 * slot_pair(1) + 5 * 640 * 2
     assert handle.ternel_tq1_gemm_workspace_bytes(64, 17408, 5120, wide, 0) == (
         counters + 256 * slot_pair(2) + 64 * 5120 * 2)
