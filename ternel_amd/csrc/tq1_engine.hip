@@ -287,8 +287,8 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
 //
 // Grid (row blocks of 256 = four 64-row tiles, batch tiles of BT, K chunks of
 // C groups). Each lane owns one row. The kernel
-//   1. issues all C x 7 word loads of its row up front (one coalesced 256-byte
-//      load per wave per word), so the whole weight stream is in flight while
+//   1. issues its row's word loads (one coalesced 256-byte load per wave per
+//      word) two blocks ahead of the block it sums, so weights stream while
 //   2. the workgroup builds the LUT23 tables of its C groups x BT vectors in
 //      LDS: 51 tasks per (vector, group) -- 25 L2 slots, 25 L3 slots, the
 //      tail -- each computing its 9 or 27 entries from 2-3 activations;
@@ -309,6 +309,8 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
 // Table tasks of one sub-chunk: 51 per (vector, group). A thread owns tasks
 // tid, tid + 256, ...; it loads their activations before anything else so the
 // in-order vmcnt wait of the build never waits behind the weight stream.
+// Blocks whose words are in flight ahead of the one being consumed.
+constexpr int kLutLoadAhead = 2;
 constexpr int lut_task_count(int c, int bt) { return bt * c * kTasksPerGroup; }
 constexpr int lut_task_iters(int c, int bt) { return (lut_task_count(c, bt) + kThreads - 1) / kThreads; }
 
@@ -448,14 +450,17 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
         //    the whole weight chunk is in flight while the tables are built.
         T xv[lut_task_iters(C, BT)][3];
         load_lut_inputs<T, C, BT>(xv, x, K, M, b0, g0, tid);
+        // Only the first kLutLoadAhead blocks' words are issued here; block
+        // c + kLutLoadAhead is issued as block c is consumed. A wave that
+        // issued all of its loads at once would stall on issue while the CU's
+        // memory queue drains, and reach its first sum only then.
         uint32_t w[C][kBlockWords];
-        {
-            const uint32_t *p = row_words + static_cast<int64_t>(g0) * kTileGroupWords;
+        const uint32_t *wp = row_words + static_cast<int64_t>(g0) * kTileGroupWords;
 #pragma unroll
-            for (int c = 0; c < C; ++c)
+        for (int c = 0; c < (kLutLoadAhead < C ? kLutLoadAhead : C); ++c)
 #pragma unroll
-                for (int j = 0; j < kBlockWords; ++j) w[c][j] = p[(c * kBlockWords + j) * kTileRows];
-        }
+            for (int j = 0; j < kBlockWords; ++j) w[c][j] = wp[(c * kBlockWords + j) * kTileRows];
+        __builtin_amdgcn_sched_barrier(0);
 
         // 2. Tables (after every lane is done reading the previous ones).
         if (g0 != g_begin) __syncthreads();
@@ -469,6 +474,12 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
         //    order -- the reference's summation order.
 #pragma unroll
         for (int c = 0; c < C; ++c) {
+            if (c + kLutLoadAhead < C) {
+#pragma unroll
+                for (int j = 0; j < kBlockWords; ++j)
+                    w[c + kLutLoadAhead][j] = wp[((c + kLutLoadAhead) * kBlockWords + j) * kTileRows];
+            }
+            __builtin_amdgcn_sched_barrier(0);
             float sum[BT];
 #pragma unroll
             for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
@@ -492,6 +503,7 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
                 sum[j] += lut[j][c][kTailBase + tail];
                 acc[j] = fmaf(scale, sum[j], acc[j]);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 

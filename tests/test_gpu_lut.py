@@ -185,3 +185,81 @@ def test_auto_configuration_meets_the_north_star_tolerance(batch: int) -> None:
     result = O.compare(got, oracle)
     assert result["normalised_max_abs_error"] < NORTH_STAR_TOLERANCE
     assert result["pattern_mismatches"] == 0
+
+
+# One vector with the split left automatic (the M = 1 decode path): K chunks
+# of four or eight groups reduced in chunk order. The shapes cover a single
+# group (no split), ragged rows, and K from 2 to 136 groups.
+AUTO_SHAPES = ((128, 128), (64, 256), (300, 640), (8192, 1024), (2048, 5120), (1024, 17408), (4096, 2048))
+
+
+def run_auto(blocks: np.ndarray, x: np.ndarray, dtype=torch.float32) -> torch.Tensor:
+    rows, g, _ = blocks.shape
+    out = tq1_matmul(pack(blocks), to_dev(x).to(dtype), layout=layout(rows, g * 128), config=MatmulConfig())
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize(("rows", "columns"), AUTO_SHAPES)
+def test_auto_split_gemv_stays_inside_the_fp32_summation_bound(rows: int, columns: int) -> None:
+    """|err| <= (128 + G) eps |W||x| elementwise, the bound of any split."""
+    groups = columns // 128
+    blocks = random_blocks(rows, columns, seed=rows + columns)
+    x = np.random.default_rng(rows * columns).normal(0.0, 1.0, size=(1, columns)).astype(np.float32)
+    got = run_auto(blocks, x).cpu().numpy()
+    oracle = O.oracle_matmul(blocks, x, rows=rows, columns=columns)
+    weights = O.dense_weights(blocks, rows=rows, columns=columns)
+    bound = (128 + groups) * float(np.finfo(np.float32).eps) * (np.abs(x.astype(np.float64)) @ np.abs(weights).T)
+    assert (np.abs(got - oracle) <= bound).all()
+    assert O.compare(got, oracle)["normalised_max_abs_error"] < NORTH_STAR_TOLERANCE
+
+
+@pytest.mark.parametrize(("rows", "columns"), AUTO_SHAPES)
+def test_auto_split_gemv_is_exact_on_integer_data(rows: int, columns: int) -> None:
+    """Unit scales and +/-1 activations: every partial and sum is an exact integer."""
+    groups = columns // 128
+    rng = np.random.default_rng(rows + 7 * columns)
+    scales = np.full(rows * groups, 1.0, dtype=np.float16).view(np.uint8).reshape(-1, 2)
+    trits = rng.integers(0, 3, size=(rows * groups, 128), dtype=np.uint8)
+    blocks = O.encode_tq1_blocks(scales, trits).reshape(rows, groups, 28)
+    x = rng.choice((-1.0, 1.0), size=(1, columns)).astype(np.float32)
+    np.testing.assert_array_equal(run_auto(blocks, x).cpu().numpy(),
+                                  O.oracle_matmul(blocks, x, rows=rows, columns=columns))
+
+
+def test_auto_split_gemv_of_one_group_is_bit_exact_against_the_lut23_oracle() -> None:
+    """One group per row leaves nothing to split: the reference order."""
+    blocks = random_blocks(200, 128, seed=5)
+    x = np.random.default_rng(5).normal(0.0, 1.0, size=(1, 128)).astype(np.float32)
+    np.testing.assert_array_equal(run_auto(blocks, x).cpu().numpy(),
+                                  O.lut23_matmul(blocks, x, rows=200, columns=128))
+
+
+def test_auto_split_gemv_is_bit_identical_between_runs() -> None:
+    blocks = random_blocks(2048, 17408, seed=77)
+    x = np.random.default_rng(77).normal(0.0, 1.0, size=(1, 17408)).astype(np.float32)
+    first = run_auto(blocks, x).cpu().numpy()
+    for _ in range(3):
+        np.testing.assert_array_equal(run_auto(blocks, x).cpu().numpy(), first)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_auto_split_gemv_rounds_once_at_the_store(dtype) -> None:
+    blocks = random_blocks(1024, 5120, seed=17)
+    raw = torch.from_numpy(np.random.default_rng(17).normal(0.0, 1.0, size=(1, 5120)).astype(np.float32)).to(dtype)
+    narrow = run_auto(blocks, raw.numpy() if dtype == torch.float16 else raw.float().numpy(), dtype=dtype)
+    assert narrow.dtype == dtype
+    wide = run_auto(blocks, raw.float().numpy())
+    np.testing.assert_array_equal(narrow.float().cpu().numpy(), wide.to(dtype).float().cpu().numpy())
+
+
+@pytest.mark.parametrize("bad", (np.nan, np.inf, -np.inf))
+@pytest.mark.parametrize("position", (0, 2600, 5119))
+def test_auto_split_gemv_carries_non_finite_activations_to_every_row(bad: float, position: int) -> None:
+    blocks = random_blocks(1024, 5120, seed=31)
+    x = np.zeros((1, 5120), dtype=np.float32)
+    x[0, position] = bad
+    got = run_auto(blocks, x).cpu().numpy()
+    want = O.oracle_matmul(blocks, x, rows=1024, columns=5120)
+    assert int(np.count_nonzero(np.isfinite(got))) == 0
+    assert O.compare(got, want)["pattern_mismatches"] == 0
