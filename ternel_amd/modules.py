@@ -111,6 +111,28 @@ class _PackedWeight(nn.Module):
             raise FormatError(f"unexpected weights: {sorted(named)}")
         return self
 
+    def load_sidecar(self, path, name: str, *, validate: bool = True) -> "_PackedWeight":
+        """Load tensor ``name`` of a canonical sidecar (src/bonsai_tq1/format.py:150-246)."""
+        from .artifact import load_sidecar_tensor
+
+        layout, packed = load_sidecar_tensor(path, name, device=self.packed.device, validate=validate)
+        self._take(layout, packed)
+        return self
+
+    def load_safetensors(self, path, name: str, *, validate: bool = True) -> "_PackedWeight":
+        """Load ``<name>.codes`` / ``<name>.scales`` of an MLX artifact (src/ternel_mlx/layout.py:37-38)."""
+        from .artifact import load_safetensors_tensor
+
+        layout, packed = load_safetensors_tensor(path, name, device=self.packed.device, validate=validate)
+        self._take(layout, packed)
+        return self
+
+    def _take(self, layout: PackedTensorLayout, packed: torch.Tensor) -> None:
+        if (layout.rows, layout.columns) != (self.layout.rows, self.layout.columns):
+            raise FormatError(f"artifact tensor is {layout.rows}x{layout.columns}, the module "
+                              f"{self.layout.rows}x{self.layout.columns}")
+        self.packed = packed
+
     @property
     def blocks(self) -> torch.Tensor:
         """Canonical ``(rows, G, 28)`` blocks, by exact inverse permutation of ``packed``."""
@@ -137,6 +159,26 @@ class PackedLinear(_PackedWeight):
         rows, columns = linear.weight.shape
         return cls(PackedTensorLayout.for_tensor(rows, columns), device=linear.weight.device)
 
+    @classmethod
+    def from_sidecar(cls, path, name: str, *, device=None) -> "PackedLinear":
+        """The sidecar tensor ``name`` as a layer (shape from its manifest entry)."""
+        from .artifact import read_sidecar, sidecar_tensors
+
+        entry = sidecar_tensors(read_sidecar(path)[1]).get(name)
+        if entry is None:
+            raise FormatError(f"sidecar has no tensor {name!r}")
+        return cls(entry.layout, device=device).load_sidecar(path, name)
+
+    @classmethod
+    def from_safetensors(cls, path, name: str, *, device=None) -> "PackedLinear":
+        """The MLX-artifact tensor ``name`` as a layer (shape from its tiled arrays)."""
+        from .artifact import load_safetensors_tensor
+
+        layout, packed = load_safetensors_tensor(path, name, device=device)
+        layer = cls(layout, device=packed.device)
+        layer.packed = packed
+        return layer
+
     def extra_repr(self) -> str:
         return (f"{self.layout.columns} -> {self.layout.rows}, tile={self.layout.tile}, "
                 f"{self.layout.bits_per_weight:.3f} bits/weight")
@@ -156,6 +198,24 @@ class PackedEmbedding(_PackedWeight):
     def from_embedding(cls, embedding: nn.Embedding, *, dtype: torch.dtype) -> "PackedEmbedding":
         rows, columns = embedding.weight.shape
         return cls(PackedTensorLayout.for_tensor(rows, columns), dtype=dtype, device=embedding.weight.device)
+
+    @classmethod
+    def from_sidecar(cls, path, name: str, *, dtype: torch.dtype, device=None) -> "PackedEmbedding":
+        from .artifact import read_sidecar, sidecar_tensors
+
+        entry = sidecar_tensors(read_sidecar(path)[1]).get(name)
+        if entry is None:
+            raise FormatError(f"sidecar has no tensor {name!r}")
+        return cls(entry.layout, dtype=dtype, device=device).load_sidecar(path, name)
+
+    @classmethod
+    def from_safetensors(cls, path, name: str, *, dtype: torch.dtype, device=None) -> "PackedEmbedding":
+        from .artifact import load_safetensors_tensor
+
+        layout, packed = load_safetensors_tensor(path, name, device=device)
+        table = cls(layout, dtype=dtype, device=packed.device)
+        table.packed = packed
+        return table
 
     def extra_repr(self) -> str:
         return f"{self.layout.rows} x {self.layout.columns}, tile={self.layout.tile}, {self.dtype}"
@@ -187,11 +247,35 @@ def replace_with_packed(model: nn.Module, *, embedding_dtype: torch.dtype = torc
     return model
 
 
+def load_packed_model(model: nn.Module, path, *, names=None) -> list[str]:
+    """Fill every packed module of ``model`` from an artifact: a canonical
+    sidecar, or an MLX safetensors file (``.safetensors``). ``names`` maps a
+    module path (``layers.0.mlp.down_proj``) to its tensor name in the
+    artifact; by default the tensor carries the module path (the MLX
+    artifact's convention, src/ternel_mlx/packed_model.py:72-92). Returns the
+    module paths loaded; a missing tensor raises FormatError."""
+    from pathlib import Path
+
+    safetensors = Path(path).suffix == ".safetensors"
+    loaded = []
+    for module_path, module in model.named_modules():
+        if not isinstance(module, _PackedWeight):
+            continue
+        tensor = names(module_path) if callable(names) else (names or {}).get(module_path, module_path)
+        if safetensors:
+            module.load_safetensors(path, tensor)
+        else:
+            module.load_sidecar(path, tensor)
+        loaded.append(module_path)
+    return loaded
+
+
 __all__ = [
     "BLOCK_BYTES",
     "LUT23_MAX_BATCH",
     "PackedEmbedding",
     "PackedLinear",
+    "load_packed_model",
     "packed_matmul",
     "replace_with_packed",
     "select_kernel",
