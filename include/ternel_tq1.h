@@ -89,6 +89,20 @@ int ternel_tq1_decode(const uint8_t *blocks, int64_t nblocks, uint8_t *scales_ou
                       void *stream);
 
 /*
+ * Q2_0/g128 source blocks (34 bytes each, as the GGUF payload stores them)
+ * re-encoded as canonical TQ1_G128 blocks on the device: the scale copied,
+ * every 2-bit code c in {0,1,2} packed base 3. Replaces decode_q2_blocks +
+ * encode_tq1_blocks (src/bonsai_tq1/format.py:51-91, run per tensor by
+ * src/bonsai_tq1/pack_model.py:72-80). *bad_codes (device u64, set by the
+ * call) receives the number of codes equal to 3, which have no ternary
+ * meaning: the reference raises "source contains N non-ternary code(s)" when
+ * it is nonzero, and the output blocks are then not to be used. No alignment
+ * is required of either buffer.
+ */
+int ternel_tq1_from_q2(const uint8_t *q2_blocks, int64_t nblocks, uint8_t *blocks, uint64_t *bad_codes,
+                       void *stream);
+
+/*
  * Canonical blocks -> packed words and back (exact permutations). Replace the
  * upload-time reorder of the reference (reorder_tensor_arrays /
  * restore_tensor_arrays, src/bonsai_tq1/lut23_reorder.py:126-165; the

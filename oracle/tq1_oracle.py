@@ -17,6 +17,11 @@ How each function is pinned (so that a plausible mistake fails a check):
   (byte 243 -> ``regular=1``, tail 27 -> ``tail=1``, every legal byte and tail
   byte round-trips, all 65,536 scale patterns survive), and planted mistakes.
 * ``encode_tq1_blocks`` -- inverse of the truth table + round trip.
+* ``decode_q2_blocks`` -- the reference's known answer (codes 0,1,2,3 repeated
+  with scale bytes 0xAA 0x55 decode in that order, tests/test_format.py:94-102),
+  a bit-by-bit pure-Python restatement over all 256 byte values at every
+  position, and the Q2 and TQ1 reference GEMVs agreeing exactly after
+  repacking (tests/test_format.py:146-158).
 * ``reorder_tensor_arrays`` / ``restore_tensor_arrays`` -- index formula on
   brute-force loops + round trip at rows {1, 48, 256, 257, 513}.
 * ``reference_gemv`` / ``lut23_matmul`` / ``oracle_matmul`` -- exact-integer
@@ -114,6 +119,31 @@ def encode_tq1_blocks(scales, codes) -> np.ndarray:
     out[:, 2:27] = (full * weights5).sum(axis=2).astype(np.uint8)
     out[:, 27] = (code_array[:, TAIL_FIRST_COLUMN:].astype(np.uint16) * weights5[:3]).sum(axis=1).astype(np.uint8)
     return out
+
+
+SOURCE_BLOCK_BYTES = 34  # src/bonsai_tq1/format.py:15
+
+
+def decode_q2_blocks(blocks) -> tuple[np.ndarray, np.ndarray]:
+    """Prism Q2_0/g128 blocks -> (scale bytes (N, 2), codes (N, 128) in 0..3).
+
+    src/bonsai_tq1/format.py:51-63: code c of a block is bits 2(c % 4) and up of
+    quant byte c // 4 (quant bytes follow the two scale bytes).
+    """
+    source = np.asarray(blocks, dtype=np.uint8)
+    if source.ndim == 1:
+        source = source.reshape(-1, SOURCE_BLOCK_BYTES)
+    quant = source[:, 2:].astype(np.uint8)
+    shifts = np.asarray([0, 2, 4, 6], dtype=np.uint8)
+    codes = ((quant[:, :, None] >> shifts) & 3).reshape(source.shape[0], BLOCK_SIZE)
+    return source[:, :2].copy(), codes.astype(np.uint8)
+
+
+def q2_dense_weights(blocks, *, rows: int, columns: int) -> np.ndarray:
+    """(code - 1) * scale of Q2 blocks in fp64 (src/bonsai_tq1/reference.py:9-52)."""
+    scales, codes = decode_q2_blocks(blocks)
+    s = scales.reshape(-1).view(np.float16).astype(np.float64)
+    return ((codes.astype(np.float64) - 1.0) * s[:, None]).reshape(rows, columns)
 
 
 def reorder_tensor_arrays(blocks: np.ndarray, *, tile: int) -> tuple[np.ndarray, np.ndarray]:

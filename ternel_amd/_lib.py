@@ -31,6 +31,7 @@ SIGNATURES = {
     "ternel_tq1_packed_words": (_i64, [_i64, _i64]),
     "ternel_tq1_validate": (_int, [_p, _i64, _p, _p]),
     "ternel_tq1_decode": (_int, [_p, _i64, _p, _p, _p]),
+    "ternel_tq1_from_q2": (_int, [_p, _i64, _p, _p, _p]),
     "ternel_tq1_interleave": (_int, [_p, _i64, _i64, _p, _p]),
     "ternel_tq1_deinterleave": (_int, [_p, _i64, _i64, _p, _p]),
     "ternel_tq1_matmul": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p, _size, _p]),

@@ -215,6 +215,49 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const uint8_t *__restr
 }
 
 // ---------------------------------------------------------------------------
+// q2_to_tq1_kernel: Q2_0/g128 blocks (34 bytes: fp16 scale, 32 bytes of 2-bit
+// codes, code c in bits 2(c%4).. of byte 2 + c/4) re-encoded as TQ1_G128 blocks
+// on the device -- decode_q2_blocks then encode_tq1_blocks of
+// src/bonsai_tq1/format.py:51-91 in one pass. One thread per (block, output
+// slot): slot 0 copies the scale, slots 1..25 pack codes 5(s-1).. as base-3
+// bytes, slot 26 the tail codes 125..127. Codes of value 3 have no ternary
+// meaning; they are counted (the caller rejects the source) and the byte is
+// written as if they were 2.
+// ---------------------------------------------------------------------------
+constexpr int kQ2BlockBytes = 34;
+constexpr int kQ2Slots = 27;  // the scale pair, 25 regular bytes, the tail byte
+
+__global__ __launch_bounds__(kThreads) void q2_to_tq1_kernel(const uint8_t *__restrict__ q2, uint8_t *__restrict__ tq1,
+                                                             int64_t nblocks, unsigned long long *bad_codes) {
+    const int64_t total = nblocks * kQ2Slots;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t n = i / kQ2Slots;
+        const int slot = static_cast<int>(i - n * kQ2Slots);
+        const uint8_t *src = q2 + n * kQ2BlockBytes;
+        uint8_t *dst = tq1 + n * kBlockBytes;
+        if (slot == 0) {
+            dst[0] = src[0];
+            dst[1] = src[1];
+            continue;
+        }
+        const int first = slot <= kFullSlots ? 5 * (slot - 1) : 125;
+        const int count = slot <= kFullSlots ? 5 : 3;
+        unsigned value = 0, power = 1, bad = 0;
+        for (int k = 0; k < count; ++k) {
+            const int c = first + k;
+            unsigned code = (src[2 + (c >> 2)] >> ((c & 3) * 2)) & 3u;
+            bad += code == 3u;
+            code = code == 3u ? 2u : code;
+            value += code * power;
+            power *= 3u;
+        }
+        dst[slot + 1] = static_cast<uint8_t>(value);
+        if (bad) atomicAdd(bad_codes, static_cast<unsigned long long>(bad));
+    }
+}
+
+// ---------------------------------------------------------------------------
 // interleave_kernel / deinterleave_kernel: canonical blocks <-> packed words.
 // One thread per packed word (writes coalesced) / per canonical word.
 // ---------------------------------------------------------------------------
@@ -2041,6 +2084,26 @@ int ternel_tq1_validate(const uint8_t *blocks, int64_t nblocks, uint64_t *counte
     if (grid > 8192) grid = 8192;
     hipLaunchKernelGGL(validate_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
                        reinterpret_cast<const uint32_t *>(blocks), nwords, cnt);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+int ternel_tq1_from_q2(const uint8_t *q2_blocks, int64_t nblocks, uint8_t *blocks, uint64_t *bad_codes,
+                       void *stream) {
+    g_last_error[0] = '\0';
+    if (!bad_codes) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (nblocks < 0) return fail(TERNEL_TQ1_EINVAL, "negative block count");
+    if (nblocks > 0 && (!q2_blocks || !blocks)) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (nblocks > INT64_MAX / kQ2Slots) return fail(TERNEL_TQ1_EINVAL, "too many blocks");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto *cnt = reinterpret_cast<unsigned long long *>(bad_codes);
+    hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(64), 0, s, cnt, 1);
+    TQ1_LAUNCH_CHECK();
+    if (nblocks == 0) return TERNEL_TQ1_OK;
+    int64_t grid = ceil_div(nblocks * kQ2Slots, kThreads);
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(q2_to_tq1_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, q2_blocks, blocks,
+                       nblocks, cnt);
     TQ1_LAUNCH_CHECK();
     return TERNEL_TQ1_OK;
 }

@@ -121,6 +121,43 @@ def validate_packed_codes(blocks) -> None:
         )
 
 
+SOURCE_BLOCK_BYTES = 34  # Prism Q2_0/g128: fp16 scale + 32 bytes of 2-bit codes
+
+
+def convert_q2_blocks(blocks):
+    """Q2_0/g128 source blocks -> canonical TQ1_G128 blocks on the GPU.
+
+    ``decode_q2_blocks`` + ``encode_tq1_blocks`` of src/bonsai_tq1/format.py
+    :51-91 in one device pass, with their shape checks and messages; a code of
+    3 (no ternary meaning) rejects the whole source. Returns numpy blocks for
+    numpy input and device blocks for tensor input, shaped (N, 28).
+    """
+    from . import _lib
+
+    if isinstance(blocks, torch.Tensor):
+        source = blocks
+    else:
+        source = torch.from_numpy(np.ascontiguousarray(np.asarray(blocks, dtype=np.uint8)))
+    if source.dtype != torch.uint8:
+        raise FormatError(f"Q2 blocks must be uint8, got {source.dtype}")
+    if source.ndim == 1:
+        if source.numel() % SOURCE_BLOCK_BYTES:
+            raise FormatError("Q2 byte length is not divisible by 34")
+        source = source.reshape(-1, SOURCE_BLOCK_BYTES)
+    if source.ndim != 2 or source.shape[1] != SOURCE_BLOCK_BYTES:
+        raise FormatError(f"expected Q2 blocks shaped (N, 34), got {tuple(source.shape)}")
+    device_source = (source if source.is_cuda else source.to(_device())).contiguous()
+    out = torch.empty((device_source.shape[0], BLOCK_BYTES), dtype=torch.uint8, device=device_source.device)
+    bad = torch.empty(1, dtype=torch.int64, device=device_source.device)
+    stream = torch.cuda.current_stream(device_source.device).cuda_stream
+    _lib.check(_lib.lib().ternel_tq1_from_q2(device_source.data_ptr(), device_source.shape[0], out.data_ptr(),
+                                             bad.data_ptr(), stream))
+    invalid = int(bad.item())
+    if invalid:
+        raise FormatError(f"source contains {invalid} non-ternary code(s)")
+    return out if isinstance(blocks, torch.Tensor) else out.cpu().numpy()
+
+
 def decode_tq1_blocks(blocks, *, validate: bool = True):
     """Decode 28-byte blocks to ``(scales (N,2) u8, codes (N,128) u8)`` on the GPU.
 

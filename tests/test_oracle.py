@@ -269,3 +269,54 @@ def test_a_dropped_tail_fails_the_tail_vector() -> None:
 def test_an_off_by_one_lut_split_fails_the_truth_table() -> None:
     bad = [((p * 57) >> 8, p - 9 * ((p * 57) >> 8)) for p in range(243)]
     assert any(tuple(TRUTH["lut23_split"][p]) != bad[p] for p in range(243))
+
+
+def q2_pack_python(scales: np.ndarray, codes: np.ndarray) -> np.ndarray:
+    """Bit-by-bit Q2_0 packer: quant byte j holds codes 4j..4j+3, code 4j+k in bits 2k, 2k+1."""
+    out = np.zeros((codes.shape[0], 34), dtype=np.uint8)
+    for n in range(codes.shape[0]):
+        out[n, 0:2] = scales[n]
+        for j in range(32):
+            byte = 0
+            for k in range(4):
+                byte |= int(codes[n, 4 * j + k]) << (2 * k)
+            out[n, 2 + j] = byte
+    return out
+
+
+def test_q2_decoder_order_known_answer() -> None:
+    """tests/test_format.py:94-102: codes 0,1,2,3 repeated, scale bytes 0xAA 0x55."""
+    codes = np.tile(np.asarray([0, 1, 2, 3], dtype=np.uint8), 32).reshape(1, 128)
+    scales = np.asarray([[0xAA, 0x55]], dtype=np.uint8)
+    source = q2_pack_python(scales, codes)
+    assert source[0, 2] == 0b11100100
+    got_scales, got_codes = O.decode_q2_blocks(source)
+    np.testing.assert_array_equal(got_scales, scales)
+    np.testing.assert_array_equal(got_codes, codes)
+
+
+def test_q2_decoder_matches_bit_extraction_for_every_byte_value() -> None:
+    source = np.zeros((256, 34), dtype=np.uint8)
+    source[:, 2:] = np.arange(256, dtype=np.uint8)[:, None]
+    source[:, 2 + 5] = np.arange(256, dtype=np.uint8)[::-1]  # a different value at one position
+    _, codes = O.decode_q2_blocks(source)
+    for v in range(256):
+        for j in range(32):
+            byte = 255 - v if j == 5 else v
+            assert [int(c) for c in codes[v, 4 * j:4 * j + 4]] == [(byte >> (2 * k)) & 3 for k in range(4)]
+
+
+def test_q2_and_tq1_dense_weights_agree_after_repacking() -> None:
+    """tests/test_format.py:146-158: the Q2 source and its TQ1 re-encoding are the same matrix."""
+    rng = np.random.default_rng(20260808)
+    rows, columns = 3, 256
+    groups = rows * columns // 128
+    scales = rng.integers(1, 0x7BFF, size=groups, dtype=np.uint16).view(np.uint8).reshape(groups, 2)
+    codes = rng.integers(0, 3, size=(groups, 128), dtype=np.uint8)
+    source = q2_pack_python(scales, codes)
+    packed = O.encode_tq1_blocks(*O.decode_q2_blocks(source))
+    np.testing.assert_array_equal(O.q2_dense_weights(source, rows=rows, columns=columns),
+                                  O.dense_weights(packed.reshape(rows, -1, 28), rows=rows, columns=columns))
+    x = rng.normal(size=columns).astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(O.reference_gemv(packed, x, rows=rows, columns=columns),
+                                  O.reference_gemv(O.encode_tq1_blocks(scales, codes), x, rows=rows, columns=columns))
