@@ -180,7 +180,7 @@ def main() -> int:
 
     from ternel_amd import synthetic
     from ternel_amd.kernels import (GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_get_rows, tq1_linear,
-                                    tq1_matmul)
+                                    tq1_matmul, tq1_swiglu)
     from ternel_amd.layout import PackedTensorLayout
     from ternel_amd.modules import select_kernel
 
@@ -368,7 +368,7 @@ def main() -> int:
 
     # ---- config 4: 64-layer weight stream + one embedding row -------------------
     if not args.no_model_stream:
-        result["model_stream"] = model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows,
+        result["model_stream"] = model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_swiglu,
                                               PackedTensorLayout, MatmulConfig, graph_of, time_graph)
 
     if not args.no_cpu_baseline:
@@ -383,10 +383,12 @@ C4_LAYERS = 64
 C4_VOCAB = 151936
 
 
-def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, PackedTensorLayout, MatmulConfig,
-                 graph_of, time_graph) -> dict:
+def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_swiglu, PackedTensorLayout,
+                 MatmulConfig, graph_of, time_graph) -> dict:
     """64 sequential layers of M=1 GEMVs (4.92 GB of packed weights,
-    larger than every cache, so each token reads them cold), then one embedding row."""
+    larger than every cache, so each token reads them cold), then one embedding row. The
+    gate+up weight (its rows alternating gate, up) runs as the fused SwiGLU, so each layer
+    also produces the MLP's activation; the packed bytes are the same."""
     layouts = [PackedTensorLayout.for_tensor(N, K) for _, K, N in C4_LAYER]
     weights = [[pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 4 + 10 * layer + i), layout=lay)
                 for i, ((_, K, N), lay) in enumerate(zip(C4_LAYER, layouts))] for layer in range(C4_LAYERS)]
@@ -398,8 +400,11 @@ def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, Packe
 
     def token_pass() -> None:
         for layer in range(C4_LAYERS):
-            for i, (_, K, _) in enumerate(C4_LAYER):
-                tq1_matmul(weights[layer][i], xs[K], layout=layouts[i], config=config)
+            for i, (name, K, _) in enumerate(C4_LAYER):
+                if name == "gate_up":
+                    tq1_swiglu(weights[layer][i], xs[K], layout=layouts[i])
+                else:
+                    tq1_matmul(weights[layer][i], xs[K], layout=layouts[i], config=config)
         tq1_get_rows(table, token, layout=table_layout, dtype=torch.float16)
 
     graph = graph_of(token_pass)
@@ -410,8 +415,9 @@ def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, Packe
     gather_us = time_graph(gather) / 100 * 1e3
     del graph, gather, weights, table
     return {
-        "workload": "BASELINE configs[4]: 64 x (QKV 5120->8192, O 8192->5120, gate+up 5120->34816, "
-                    "down 17408->5120) M=1 GEMVs + 1 embedding row of 151936x5120, one HIP graph per token",
+        "workload": "BASELINE configs[4]: 64 x (QKV 5120->8192, O 8192->5120, gate+up 5120->34816 with the "
+                    "fused SwiGLU epilogue, down 17408->5120) M=1 GEMVs + 1 embedding row of 151936x5120, "
+                    "one HIP graph per token",
         "packed_bytes": total,
         "ms_per_token": round(ms, 4),
         "GB/s": round(total / (ms * 1e-3) / 1e9, 1),

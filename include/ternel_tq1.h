@@ -178,6 +178,24 @@ int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M,
                       int64_t columns, int dtype, void *ws, size_t ws_bytes, void *stream);
 size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype);
 
+/*
+ * A SwiGLU MLP's gate and up projections as one packed weight, with the
+ * elementwise step fused: z[m][r] = SiLU(g) * u, where g and u are rows 2r and
+ * 2r + 1 of x @ W^T (the packed weight's rows alternate gate, up -- see
+ * ternel_amd.layout.interleave_gate_up) rounded to the activation type as the
+ * two unfused layers would return them, and SiLU(g) * u is computed in fp32.
+ * z is [M][rows / 2] in the activation type. No counterpart in the reference
+ * (its MLP runs gate_proj, up_proj and the activation as separate mlx ops,
+ * src/ternel_mlx/packed_model.py:72-92); this is the fused-MLP epilogue of its
+ * scope table's next rows. Batches up to 4 (and bf16/fp32 activations) run the
+ * LUT23 kernel with the pair exchange in its epilogue; larger fp16 batches run
+ * the GEMM into the workspace and one elementwise pass. Workspace from
+ * ternel_tq1_swiglu_workspace_bytes, same contract as ternel_tq1_linear's.
+ */
+int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M, int64_t rows, int64_t columns,
+                      int dtype, void *ws, size_t ws_bytes, void *stream);
+size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype);
+
 #ifdef __cplusplus
 }
 #endif

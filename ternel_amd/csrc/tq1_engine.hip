@@ -28,6 +28,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "ternel_tq1.h"
 
 namespace {
@@ -462,7 +464,16 @@ __device__ __forceinline__ float sum_partials_in_order(const float *src, int64_t
 // s_waitcnt with vmcnt(0) and the other counters left alone (gfx9 encoding).
 __device__ __forceinline__ void wait_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
-template <typename T, int C, int BT>
+// SiLU(g) * u of a gate/up pair, in fp32 from the two outputs as the unfused
+// layers would round them (the activation type): the elementwise step of a
+// SwiGLU MLP applied to the linear's outputs.
+template <typename T>
+__device__ __forceinline__ T swiglu_pair(T gate, T up) {
+    const float g = to_f32<T>(gate);
+    return from_f32<T>(g / (1.0f + expf(-g)) * to_f32<T>(up));
+}
+
+template <typename T, int C, int BT, bool GLU = false>
 __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
     const uint32_t *__restrict__ packed, const T *__restrict__ x, T *__restrict__ y,
     float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
@@ -550,13 +561,24 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
         }
     }
 
-    // 4. Output.
-    if (k_split == 1) {
-        if (row_ok) {
-#pragma unroll
-            for (int j = 0; j < BT; ++j)
-                if (b0 + j < M) y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(acc[j]);
+    // 4. Output. With GLU, rows 2r and 2r+1 are the gate and up rows of one
+    // SwiGLU unit and sit in adjacent lanes: each lane rounds its value as the
+    // unfused linear would, the even lane takes its partner's and writes
+    // SiLU(gate) * up to y[r] of an N/2-wide output. Every lane takes part in
+    // the exchange.
+    auto store = [&](int j, float v) {
+        if constexpr (GLU) {
+            const T own = from_f32<T>(v);
+            const float partner = __shfl_xor(to_f32<T>(own), 1, 64);
+            if (row_ok && (lane & 1) == 0 && b0 + j < M)
+                y[static_cast<int64_t>(b0 + j) * (N / 2) + row / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
+        } else {
+            if (row_ok && b0 + j < M) y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(v);
         }
+    };
+    if (k_split == 1) {
+#pragma unroll
+        for (int j = 0; j < BT; ++j) store(j, acc[j]);
         return;
     }
     // Split: publish the partial with agent-coherent stores (they bypass the
@@ -578,16 +600,24 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
                  static_cast<unsigned>(k_split - 1);
     __syncthreads();
     if (!s_last) return;
-    if (row_ok) {
-        const int64_t stride = static_cast<int64_t>(M) * N;
+    const int64_t stride = static_cast<int64_t>(M) * N;
 #pragma unroll
-        for (int j = 0; j < BT; ++j) {
-            if (b0 + j >= M) continue;
-            const float *src = partial + static_cast<int64_t>(b0 + j) * N + row;
-            y[static_cast<int64_t>(b0 + j) * N + row] = from_f32<T>(sum_partials_in_order(src, stride, k_split));
-        }
+    for (int j = 0; j < BT; ++j) {
+        const float *src = partial + static_cast<int64_t>(b0 + j) * N + row;
+        store(j, row_ok && b0 + j < M ? sum_partials_in_order(src, stride, k_split) : 0.0f);
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The elementwise SwiGLU step over a linear's output whose rows alternate
+// gate, up: z[i] = SiLU(y[2i]) * y[2i+1] (N even, so pairs never straddle a
+// batch row).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const T *__restrict__ y, T *__restrict__ z,
+                                                                int64_t pairs) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < pairs;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        z[i] = swiglu_pair<T>(y[2 * i], y[2 * i + 1]);
 }
 
 template <typename T>
@@ -1739,23 +1769,38 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
     return TERNEL_TQ1_OK;
 }
 
-template <typename T, int C, int BT>
+template <typename T, int C, int BT, bool GLU = false>
 void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *x, void *y, float *partial,
                        unsigned *counters, int64_t M, int64_t rows, int G, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.batch_tiles),
                     static_cast<unsigned>(plan.k_split));
-    hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT>), grid, dim3(kThreads), 0, stream, packed,
+    hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU>), grid, dim3(kThreads), 0, stream, packed,
                        static_cast<const T *>(x), static_cast<T *>(y), partial, counters, static_cast<int>(M),
                        static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
 }
 
 template <typename T>
 int launch_lut(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
-               const LutPlan &plan, void *ws, hipStream_t stream) {
+               const LutPlan &plan, void *ws, hipStream_t stream, bool glu = false) {
     const int G = static_cast<int>(columns / kBlockWeights);
     unsigned *counters = plan.k_split > 1 ? static_cast<unsigned *>(ws) : nullptr;
     float *partial =
         plan.k_split > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + plan.counter_bytes) : nullptr;
+    if (glu) {  // SwiGLU epilogue: one vector per workgroup
+#define TQ1_LUT_GLU_CASE(CC)                                                                          \
+        if (plan.chunk == CC && plan.batch_tile == 1) {                                               \
+            launch_lut_kernel<T, CC, 1, true>(plan, packed, x, y, partial, counters, M, rows, G, stream); \
+            TQ1_LAUNCH_CHECK();                                                                       \
+            return TERNEL_TQ1_OK;                                                                     \
+        }
+        TQ1_LUT_GLU_CASE(1)
+        TQ1_LUT_GLU_CASE(2)
+        TQ1_LUT_GLU_CASE(4)
+        TQ1_LUT_GLU_CASE(8)
+#undef TQ1_LUT_GLU_CASE
+        return fail(TERNEL_TQ1_EINVAL, "no SwiGLU LUT23 kernel for chunk %d, batch tile %d", plan.chunk,
+                    plan.batch_tile);
+    }
 #define TQ1_LUT_CASE(CC, BB)                                                                         \
     if (plan.chunk == CC && plan.batch_tile == BB) {                                                 \
         launch_lut_kernel<T, CC, BB>(plan, packed, x, y, partial, counters, M, rows, G, stream);     \
@@ -2300,6 +2345,68 @@ int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M,
     if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
         return ternel_tq1_matmul(packed, x, y, M, rows, columns, dtype, 0, 0, ws, ws_bytes, stream);
     return ternel_tq1_gemm(packed, x, y, M, rows, columns, dtype, TERNEL_TQ1_GEMM_AUTO, 0, ws, ws_bytes, stream);
+}
+
+// Where the GEMM path's fp16 gate/up output sits in the workspace: after the
+// GEMM's own workspace and never inside the counter region that every call
+// expects to find zero.
+static size_t swiglu_pairs_offset(int64_t M, int64_t rows, int64_t columns) {
+    const size_t gemm = ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
+    return (std::max(gemm, kCounterRegionBytes) + 255) / 256 * 256;
+}
+
+size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
+    if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK || rows % 2) return 0;
+    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
+        return ternel_tq1_matmul_workspace_bytes(M, rows, columns, 1, 0);
+    return swiglu_pairs_offset(M, rows, columns) + static_cast<size_t>(M) * rows * sizeof(_Float16);
+}
+
+int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M, int64_t rows, int64_t columns,
+                      int dtype, void *ws, size_t ws_bytes, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
+    if (rows % 2)
+        return fail(TERNEL_TQ1_EINVAL, "a SwiGLU weight interleaves gate and up rows, so its rows must be even, got %lld",
+                    static_cast<long long>(rows));
+    if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+    if (!x || !z) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16) {
+        LutPlan plan;
+        if ((rc = plan_lut(M, rows, columns, 1, 0, &plan)) != TERNEL_TQ1_OK) return rc;
+        if (plan.batch_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");
+        const size_t need = plan.counter_bytes + plan.partial_bytes;
+        if (need && (!ws || ws_bytes < need))
+            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
+                        need);
+        switch (dtype) {
+            case TERNEL_TQ1_F16:
+                return launch_lut<_Float16>(packed, x, z, M, rows, columns, plan, ws, s, true);
+            case TERNEL_TQ1_BF16:
+                return launch_lut<bf16_t>(packed, x, z, M, rows, columns, plan, ws, s, true);
+            default:
+                return launch_lut<float>(packed, x, z, M, rows, columns, plan, ws, s, true);
+        }
+    }
+    const size_t need = ternel_tq1_swiglu_workspace_bytes(M, rows, columns, dtype);
+    if (need == 0 || !ws || ws_bytes < need)
+        return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu a SwiGLU GEMM needs", ws_bytes,
+                    need);
+    const size_t gemm = ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
+    void *pairs = static_cast<char *>(ws) + swiglu_pairs_offset(M, rows, columns);
+    if ((rc = ternel_tq1_gemm(packed, x, pairs, M, rows, columns, dtype, TERNEL_TQ1_GEMM_AUTO, 0, gemm ? ws : nullptr,
+                              gemm, stream)) != TERNEL_TQ1_OK)
+        return rc;
+    const int64_t count = M * (rows / 2);
+    int64_t grid = ceil_div(count, kThreads);
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL((swiglu_pairs_kernel<_Float16>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
+                       static_cast<const _Float16 *>(pairs), static_cast<_Float16 *>(z), count);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
 }
 
 }  // extern "C"

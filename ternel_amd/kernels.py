@@ -244,6 +244,28 @@ def tq1_linear(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLay
     return out
 
 
+def tq1_swiglu(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+    """SiLU(gate) * up of a SwiGLU MLP whose gate and up projections are one
+    packed weight with alternating rows (``layout.interleave_gate_up``):
+    ``(batch, rows // 2)`` in ``x.dtype``, each gate/up value rounded to
+    ``x.dtype`` as the unfused layers would return it."""
+    check_packed(packed, layout=layout)
+    batch = check_activations(x, layout=layout)
+    if layout.rows % 2:
+        raise FormatError(f"a SwiGLU weight interleaves gate and up rows, so its rows must be even, "
+                          f"got {layout.rows}")
+    x = x.contiguous()
+    out = torch.empty((batch, layout.rows // 2), dtype=x.dtype, device=x.device)
+    handle = _lib.lib()
+    code = _DTYPE_CODE[x.dtype]
+    need = handle.ternel_tq1_swiglu_workspace_bytes(batch, layout.rows, layout.columns, code)
+    ws = workspace(x.device, need)
+    _lib.check(handle.ternel_tq1_swiglu(
+        packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns, code,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(x.device)))
+    return out
+
+
 def tq1_get_rows(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
                  dtype: torch.dtype) -> torch.Tensor:
     """Decode the rows named by ``indices`` (1-D); reference tq1_get_rows, kernels.py:1360-1398.

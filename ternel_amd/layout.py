@@ -165,6 +165,19 @@ def unpack_blocks(codes: np.ndarray, scales: np.ndarray, *, layout: PackedTensor
     return out.reshape(layout.canonical_shape)
 
 
+def interleave_gate_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """Canonical blocks of a SwiGLU MLP's gate and up projections, (rows, G, 28)
+    each, as one ``(2 rows, G, 28)`` weight whose rows alternate gate, up: row
+    2r is gate row r and row 2r + 1 up row r, the order the fused SwiGLU
+    epilogue pairs them in."""
+    g, u = np.asarray(gate), np.asarray(up)
+    if g.dtype != np.uint8 or u.dtype != np.uint8:
+        raise FormatError("gate and up blocks must be uint8")
+    if g.shape != u.shape or g.ndim != 3 or g.shape[2] != BLOCK_BYTES:
+        raise FormatError(f"gate {g.shape} and up {u.shape} must be canonical blocks of one shape")
+    return np.stack([g, u], axis=1).reshape(2 * g.shape[0], g.shape[1], BLOCK_BYTES)
+
+
 @dataclass(frozen=True)
 class ModelLinearShape:
     """One distinct linear shape of Ternary Bonsai 27B (src/ternel_mlx/layout.py:151-176)."""

@@ -30,9 +30,10 @@ from .kernels import (
     tq1_gemm,
     tq1_get_rows,
     tq1_matmul,
+    tq1_swiglu,
     unpack_weights,
 )
-from .layout import PackedTensorLayout, pack_blocks, unpack_blocks
+from .layout import PackedTensorLayout, interleave_gate_up, pack_blocks, unpack_blocks
 
 # Dispatch (src/ternel_mlx/modules.py:331-422, re-measured for MI355X): the
 # LUT23 kernel for batches up to LUT23_MAX_BATCH, the MFMA kernel above it.
@@ -231,6 +232,67 @@ class PackedEmbedding(_PackedWeight):
         return packed_matmul(self.packed, x, layout=self.layout)
 
 
+class PackedSwiGLU(nn.Module):
+    """The gate and up projections of a SwiGLU MLP as one packed weight, with
+    the elementwise step fused: ``forward(x) = SiLU(x @ gate.T) * (x @ up.T)``,
+    each projection rounded to ``x.dtype`` as the unfused layers would return
+    it. The weight's rows alternate gate, up (``layout.interleave_gate_up``);
+    one launch reads both projections' 28-byte blocks and writes ``hidden``
+    values per vector. No counterpart module in the reference (its MLP runs the
+    two packed linears and the activation separately)."""
+
+    def __init__(self, hidden: int, columns: int, device=None) -> None:
+        super().__init__()
+        self.layout = PackedTensorLayout.for_tensor(2 * hidden, columns)
+        self.hidden = hidden
+        if device is None and torch.cuda.is_available():
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.register_buffer("packed", torch.zeros(packed_shape(self.layout), dtype=torch.int32, device=device))
+
+    @classmethod
+    def from_linears(cls, gate: nn.Linear, up: nn.Linear) -> "PackedSwiGLU":
+        if gate.bias is not None or up.bias is not None:
+            raise FormatError("a packed linear layer cannot carry a bias")
+        if gate.weight.shape != up.weight.shape:
+            raise FormatError(f"gate {tuple(gate.weight.shape)} and up {tuple(up.weight.shape)} differ")
+        hidden, columns = gate.weight.shape
+        return cls(hidden, columns, device=gate.weight.device)
+
+    def load_blocks(self, gate, up, *, validate: bool = True) -> "PackedSwiGLU":
+        """Canonical ``(hidden, G, 28)`` blocks of each projection."""
+        from .artifact import upload
+
+        def host(blocks):
+            return blocks.cpu().numpy() if isinstance(blocks, torch.Tensor) else np.asarray(blocks)
+
+        fused = interleave_gate_up(host(gate), host(up))
+        self.packed = upload(fused, self.layout, device=self.packed.device, validate=validate)
+        return self
+
+    def load_sidecar(self, path, gate: str, up: str) -> "PackedSwiGLU":
+        from .artifact import read_sidecar, sidecar_blocks, sidecar_tensors
+
+        tensors = sidecar_tensors(read_sidecar(path)[1])
+        for name in (gate, up):
+            if name not in tensors:
+                raise FormatError(f"sidecar has no tensor {name!r}")
+        return self.load_blocks(sidecar_blocks(path, tensors[gate]), sidecar_blocks(path, tensors[up]))
+
+    def load_safetensors(self, path, gate: str, up: str) -> "PackedSwiGLU":
+        from .artifact import safetensors_blocks
+
+        return self.load_blocks(safetensors_blocks(path, gate)[1], safetensors_blocks(path, up)[1])
+
+    def extra_repr(self) -> str:
+        return f"{self.layout.columns} -> 2 x {self.hidden} -> {self.hidden}, SiLU(gate) * up"
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.shape[-1] != self.layout.columns:
+            raise FormatError(f"activations have {x.shape[-1]} columns, expected {self.layout.columns}")
+        flat = x.reshape(-1, self.layout.columns)
+        return tq1_swiglu(self.packed, flat, layout=self.layout).reshape(*x.shape[:-1], self.hidden)
+
+
 def replace_with_packed(model: nn.Module, *, embedding_dtype: torch.dtype = torch.float16) -> nn.Module:
     """Swap every bias-free ``nn.Linear`` and every ``nn.Embedding`` for its packed twin.
 
@@ -275,6 +337,7 @@ __all__ = [
     "LUT23_MAX_BATCH",
     "PackedEmbedding",
     "PackedLinear",
+    "PackedSwiGLU",
     "load_packed_model",
     "packed_matmul",
     "replace_with_packed",

@@ -198,3 +198,15 @@ def test_missing_tensor_names_are_reported(tmp_path) -> None:
     save_safetensors(path, {"a": random_blocks(4, 1, seed=9)})
     with pytest.raises(FormatError, match="no packed tensor 'b'"):
         safetensors_blocks(path, "b")
+
+
+def test_interleave_gate_up_alternates_rows() -> None:
+    from ternel_amd.layout import interleave_gate_up
+
+    gate, up = random_blocks(5, 2, seed=20), random_blocks(5, 2, seed=21)
+    fused = interleave_gate_up(gate, up)
+    assert fused.shape == (10, 2, 28)
+    np.testing.assert_array_equal(fused[0::2], gate)
+    np.testing.assert_array_equal(fused[1::2], up)
+    with pytest.raises(FormatError, match="one shape"):
+        interleave_gate_up(gate, up[:4])
