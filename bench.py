@@ -366,6 +366,22 @@ def main() -> int:
                 del g, blk, xp
             result[f"prefill_m{M}"] = prefill
 
+    # ---- the tied output head at M=1 (scope row f3): the largest GEMV of a token --
+    if not args.no_model_stream:
+        head_layout = PackedTensorLayout.for_tensor(HEAD_ROWS, 5120)
+        heads = [pack_weights(synthetic.device_blocks(HEAD_ROWS, 5120, seed=synthetic.SEED_BASE + 50 + i),
+                              layout=head_layout) for i in range(2)]  # 2 x 278 MB: every launch reads HBM
+        xh = synthetic.device_activations(1, 5120, seed=synthetic.SEED_BASE + 51)
+        g = graph_of(lambda: [tq1_matmul(heads[s % 2], xh, layout=head_layout, config=MatmulConfig())
+                              for s in range(20)])
+        ms = time_graph(g) / 20
+        head_bytes = packed_bytes(5120, HEAD_ROWS)
+        result["head_m1"] = {"workload": f"tied output head {HEAD_ROWS}x5120 at M=1 (PackedEmbedding.as_linear, "
+                                         "two alternating copies)",
+                             "us": round(ms * 1e3, 2), "GB/s": round(head_bytes / (ms * 1e-3) / 1e9, 1),
+                             "frac_of_hbm_peak": round(head_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del g, heads
+
     # ---- config 4: 64-layer weight stream + one embedding row -------------------
     if not args.no_model_stream:
         result["model_stream"] = model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_swiglu,
@@ -381,6 +397,7 @@ def main() -> int:
 C4_LAYER = (("qkv", 5120, 8192), ("o", 8192, 5120), ("gate_up", 5120, 34816), ("down", 17408, 5120))
 C4_LAYERS = 64
 C4_VOCAB = 151936
+HEAD_ROWS = 248320  # Bonsai 27B vocabulary: the tied lm_head (src/ternel_mlx/layout.py:179-192 census)
 
 
 def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_swiglu, PackedTensorLayout,
