@@ -146,7 +146,9 @@ size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t column
  *                          LDS, K split stream-K over one workgroup per CU
  *                          with an ordered in-launch reduction (k_split must
  *                          be 0/1; columns < 2^22);
- *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 32, WIDE above (TILE if k_split > 1).
+ *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 32; above, WIDE when it has at
+ *                          least CUs/4 output tiles or 15 (tile, group) steps
+ *                          per CU, TILE otherwise (and when k_split > 1).
  * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. k_split divides
  * columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
  * same 64 KiB counter region + fp32 partials contract as ternel_tq1_matmul.
@@ -177,6 +179,16 @@ int ternel_tq1_get_rows(const uint32_t *packed, int64_t rows, int64_t columns, c
 int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
                       int64_t columns, int dtype, void *ws, size_t ws_bytes, void *stream);
 size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype);
+
+/*
+ * The kernel ternel_tq1_linear launches for this shape: TERNEL_TQ1_KERNEL_LUT23
+ * or one of the TERNEL_TQ1_GEMM_* forms (never AUTO); negative on a rejected
+ * shape or dtype. Host-only, touches no device. The counterpart of the
+ * reference's select_gemm / select_lut23 decisions (src/ternel_mlx/modules.py
+ * :320-423), exposed so that a dispatch sweep can be replayed through the rule.
+ */
+#define TERNEL_TQ1_KERNEL_LUT23 100
+int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype);
 
 /*
  * A SwiGLU MLP's gate and up projections as one packed weight, with the

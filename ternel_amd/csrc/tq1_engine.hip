@@ -2075,21 +2075,42 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
     }
 }
 
-// Automatic choice (measured on MI355X over the 27B shapes): the direct form
-// up to 32 activation rows, the wide form above -- 64-row tiles beat the
-// direct form at M = 64 (gate/up 37.6 us against 53.2) and the wide form
-// beats the tile form at every prefill shape -- unless a fixed K split is
-// asked for or the rows are too long for its 32-bit buffer offsets.
+// Automatic choice, from a sweep of every form over the 27B linears on MI355X
+// (the fixture tests/golden/dispatch_sweep_mi355x.json replays it): the direct
+// form up to 32 activation rows; above, the wide form when stream-K has enough
+// tiles or enough work per CU to amortise its reduction -- at least CUs/4
+// tiles (a tile's partials come from at most ~4 contributors) or 15 (tile,
+// group) steps per CU -- and the fixed-split tile form otherwise (QKV
+// 5120->8192 M=128: 30.4 us against 45.8; gate/up 5120->17408 M=128: 48.7
+// against 57.7 the other way). The tile form also serves a fixed K split and
+// rows too long for the wide form's 32-bit buffer offsets.
 constexpr int64_t kAutoDirectMaxBatch = 32;
-int resolve_gemm_form(int64_t M, int64_t columns, int form, int k_split) {
+int wide_blocks(int64_t M, int64_t tiles_n, int64_t groups, int64_t cus);
+int device_cu_count();
+int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (form != TERNEL_TQ1_GEMM_AUTO) return form;
     if (M <= kAutoDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
-    return k_split <= 1 && columns <= kWideMaxColumns ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_TILE;
+    if (k_split > 1 || columns > kWideMaxColumns) return TERNEL_TQ1_GEMM_TILE;
+    const int64_t cus = device_cu_count();
+    const int64_t groups = columns / kBlockWeights;
+    const int64_t tiles_n = ceil_div(rows, kWideRows);
+    const int nb = wide_blocks(M, tiles_n, groups, cus);
+    const int64_t tiles = tiles_n * ceil_div(M, 32 * nb);
+    return 4 * tiles >= cus || tiles * groups >= 15 * cus ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_TILE;
 }
 
-// The dispatch rule of packed_matmul, retuned for MI355X: the LUT23 kernel up
-// to this many activation rows, the MFMA kernels above it (fp16 only).
+// The dispatch rule of packed_matmul, retuned for MI355X by the same sweep: the
+// LUT23 kernel up to 4 activation rows -- 6 for matrices under 16 MiB of
+// packed weights, where the MFMA forms' fixed costs weigh more (O 8192->5120
+// M=5: 13.9 us against 16.6) -- the MFMA kernels above it (fp16 only).
 constexpr int64_t kLinearLutMaxBatch = 4;
+constexpr int64_t kLinearLutMaxBatchSmall = 6;
+constexpr int64_t kLinearSmallMatrixBytes = 16ll << 20;
+bool linear_uses_lut(int64_t M, int64_t rows, int64_t columns, int dtype) {
+    if (dtype != TERNEL_TQ1_F16) return true;
+    const int64_t bytes = rows * (columns / kBlockWeights) * kBlockBytes;
+    return M <= (bytes < kLinearSmallMatrixBytes ? kLinearLutMaxBatchSmall : kLinearLutMaxBatch);
+}
 
 int check_packed_pointer(const void *packed) {
     if (!packed) return fail(TERNEL_TQ1_EINVAL, "null pointer");
@@ -2232,7 +2253,7 @@ int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M,
 
 size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
-    form = resolve_gemm_form(M, columns, form, k_split);
+    form = resolve_gemm_form(M, rows, columns, form, k_split);
     if (form == TERNEL_TQ1_GEMM_DIRECT) {
         DirectPlan direct;
         if (plan_direct(M, rows, columns, k_split, &direct) != TERNEL_TQ1_OK) return 0;
@@ -2260,7 +2281,7 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
     if (form != TERNEL_TQ1_GEMM_AUTO && form != TERNEL_TQ1_GEMM_TILE && form != TERNEL_TQ1_GEMM_DIRECT &&
         form != TERNEL_TQ1_GEMM_WIDE)
         return fail(TERNEL_TQ1_EINVAL, "unknown GEMM form %d", form);
-    form = resolve_gemm_form(M, columns, form, k_split);
+    form = resolve_gemm_form(M, rows, columns, form, k_split);
     if (form == TERNEL_TQ1_GEMM_DIRECT) {
         DirectPlan direct;
         if ((rc = plan_direct(M, rows, columns, k_split, &direct)) != TERNEL_TQ1_OK) return rc;
@@ -2335,14 +2356,14 @@ int ternel_tq1_get_rows(const uint32_t *packed, int64_t rows, int64_t columns, c
 }
 
 size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
-    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
+    if (linear_uses_lut(M, rows, columns, dtype))
         return ternel_tq1_matmul_workspace_bytes(M, rows, columns, 0, 0);
     return ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
 }
 
 int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
                       int dtype, void *ws, size_t ws_bytes, void *stream) {
-    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
+    if (linear_uses_lut(M, rows, columns, dtype))
         return ternel_tq1_matmul(packed, x, y, M, rows, columns, dtype, 0, 0, ws, ws_bytes, stream);
     return ternel_tq1_gemm(packed, x, y, M, rows, columns, dtype, TERNEL_TQ1_GEMM_AUTO, 0, ws, ws_bytes, stream);
 }
@@ -2355,9 +2376,18 @@ static size_t swiglu_pairs_offset(int64_t M, int64_t rows, int64_t columns) {
     return (std::max(gemm, kCounterRegionBytes) + 255) / 256 * 256;
 }
 
+int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
+    if (linear_uses_lut(M, rows, columns, dtype)) return TERNEL_TQ1_KERNEL_LUT23;
+    return resolve_gemm_form(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
+}
+
 size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK || rows % 2) return 0;
-    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16)
+    if (linear_uses_lut(M, rows, columns, dtype))
         return ternel_tq1_matmul_workspace_bytes(M, rows, columns, 1, 0);
     return swiglu_pairs_offset(M, rows, columns) + static_cast<size_t>(M) * rows * sizeof(_Float16);
 }
@@ -2374,7 +2404,7 @@ int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M,
     if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
     if (!x || !z) return fail(TERNEL_TQ1_EINVAL, "null pointer");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (M <= kLinearLutMaxBatch || dtype != TERNEL_TQ1_F16) {
+    if (linear_uses_lut(M, rows, columns, dtype)) {
         LutPlan plan;
         if ((rc = plan_lut(M, rows, columns, 1, 0, &plan)) != TERNEL_TQ1_OK) return rc;
         if (plan.batch_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");

@@ -36,18 +36,24 @@ from .kernels import (
 from .layout import PackedTensorLayout, interleave_gate_up, pack_blocks, unpack_blocks
 
 # Dispatch (src/ternel_mlx/modules.py:331-422, re-measured for MI355X): the
-# LUT23 kernel for batches up to LUT23_MAX_BATCH, the MFMA kernel above it.
-# The LUT kernel's cost grows linearly with the batch (one table set per
-# vector) while its bytes do not, so it only pays while the weight stream
-# dominates; the MFMA kernel decodes each weight once per 128-row batch tile.
+# LUT23 kernel for small batches, the MFMA kernels above them. The LUT kernel's
+# cost grows linearly with the batch (one table set per vector) while its bytes
+# do not, so it only pays while the weight stream dominates. The rule lives in
+# the library (ternel_tq1_linear_kernel, replayed against a measured sweep in
+# tests/test_dispatch.py); LUT23_MAX_BATCH is its bound for the 27B MLP shapes.
 LUT23_MAX_BATCH = 4
+_KERNEL_NAMES = {100: "lut23", 1: "gemm", 2: "gemm", 3: "gemm"}
 
 
 def select_kernel(layout: PackedTensorLayout, batch: int, dtype: torch.dtype) -> str:
-    """``"lut23"`` or ``"gemm"`` for ``batch`` activation rows."""
-    if batch <= LUT23_MAX_BATCH or dtype != torch.float16:
-        return "lut23"
-    return "gemm"
+    """``"lut23"`` or ``"gemm"`` for ``batch`` activation rows: the library's own choice."""
+    from . import _lib
+    from .kernels import _DTYPE_CODE
+
+    code = _lib.lib().ternel_tq1_linear_kernel(batch, layout.rows, layout.columns, _DTYPE_CODE[dtype])
+    if code < 0:
+        raise FormatError(_lib.lib().ternel_tq1_last_error().decode())
+    return _KERNEL_NAMES[code]
 
 
 def packed_matmul(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
