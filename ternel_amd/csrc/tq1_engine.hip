@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "ternel_tq1.h"
 
@@ -357,16 +358,16 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
 // Blocks whose words are in flight ahead of the one being consumed.
 constexpr int kLutLoadAhead = 2;
 constexpr int lut_task_count(int c, int bt) { return bt * c * kTasksPerGroup; }
-constexpr int lut_task_iters(int c, int bt) { return (lut_task_count(c, bt) + kThreads - 1) / kThreads; }
+constexpr int lut_task_iters(int c, int bt, int threads) { return (lut_task_count(c, bt) + threads - 1) / threads; }
 
-template <typename T, int C, int BT>
-__device__ __forceinline__ void load_lut_inputs(T (&xv)[lut_task_iters(C, BT)][3], const T *__restrict__ x,
+template <typename T, int C, int BT, int NT>
+__device__ __forceinline__ void load_lut_inputs(T (&xv)[lut_task_iters(C, BT, NT)][3], const T *__restrict__ x,
                                                 int64_t K, int M, int b0, int g0, int tid) {
 #pragma unroll
-    for (int it = 0; it < lut_task_iters(C, BT); ++it) {
+    for (int it = 0; it < lut_task_iters(C, BT, NT); ++it) {
         // Clamped rather than skipped: every load issues unconditionally, which
         // keeps the compiler's vmcnt accounting exact (no branch around loads).
-        const int task = min(tid + it * kThreads, lut_task_count(C, BT) - 1);
+        const int task = min(tid + it * NT, lut_task_count(C, BT) - 1);
         const int j = task / (C * kTasksPerGroup);
         const int rem = task - j * (C * kTasksPerGroup);
         const int c = rem / kTasksPerGroup;
@@ -382,13 +383,13 @@ __device__ __forceinline__ void load_lut_inputs(T (&xv)[lut_task_iters(C, BT)][3
     }
 }
 
-template <typename T, int C, int BT>
+template <typename T, int C, int BT, int NT>
 __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
-                                                 const T (&xv)[lut_task_iters(C, BT)][3], int tid) {
+                                                 const T (&xv)[lut_task_iters(C, BT, NT)][3], int tid) {
 #pragma unroll
-    for (int it = 0; it < lut_task_iters(C, BT); ++it) {
+    for (int it = 0; it < lut_task_iters(C, BT, NT); ++it) {
         // A clamped (repeated) task writes the same values to the same entries.
-        const int task = min(tid + it * kThreads, lut_task_count(C, BT) - 1);
+        const int task = min(tid + it * NT, lut_task_count(C, BT) - 1);
         const int j = task / (C * kTasksPerGroup);
         const int rem = task - j * (C * kTasksPerGroup);
         const int c = rem / kTasksPerGroup;
@@ -421,18 +422,24 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split_pair(uint32_t pair, uint32_t &lo_a, uint32_t &hi_a, uint32_t &lo_b,
                                            uint32_t &hi_b) {
     u16x2 p = __builtin_bit_cast(u16x2, pair);
-    const u16x2 h = (p * static_cast<unsigned short>(57)) >> static_cast<unsigned short>(9);
+    u16x2 h = (p * static_cast<unsigned short>(57)) >> static_cast<unsigned short>(9);
     const u16x2 l = p - h * static_cast<unsigned short>(9);
+    // Hide h's range (< 32) from the compiler: with it known, the low half is
+    // unpacked as (h & 31) << 2, two instructions, instead of one SDWA shift.
+    uint32_t hb = __builtin_bit_cast(uint32_t, h);
+    asm volatile("" : "+v"(hb));
+    h = __builtin_bit_cast(u16x2, hb);
     lo_a = l.x;
     hi_a = h.x;
     lo_b = l.y;
     hi_b = h.y;
 }
 
-// All four bytes of a block word: lo/hi for byte b of the word.
+// All four bytes of a block word: lo/hi for byte b of the word. Bytes 1 and 3
+// move to the 16-bit halves with one byte permute (selector 0x0c = zero).
 __device__ __forceinline__ void split_word(uint32_t word, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
-    split_pair(word & 0x00ff00ffu, lo[0], hi[0], lo[2], hi[2]);         // bytes 0 and 2
-    split_pair((word >> 8) & 0x00ff00ffu, lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
+    split_pair(word & 0x00ff00ffu, lo[0], hi[0], lo[2], hi[2]);                           // bytes 0 and 2
+    split_pair(__builtin_amdgcn_perm(0u, word, 0x0c030c01u), lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
 }
 
 // Adds partial[0..k) (stride apart) left to right. The agent-coherent loads of
@@ -473,19 +480,33 @@ __device__ __forceinline__ T swiglu_pair(T gate, T up) {
     return from_f32<T>(g / (1.0f + expf(-g)) * to_f32<T>(up));
 }
 
-template <typename T, int C, int BT, bool GLU = false>
-__global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
+template <typename T, int C, int BT, bool GLU = false, int KW = 1>
+__global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     const uint32_t *__restrict__ packed, const T *__restrict__ x, T *__restrict__ y,
     float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
     int k_split) {
+    // KW waves share each 64-row tile: wave stream s sums blocks
+    // [s * CB, (s + 1) * CB) of every sub-chunk, so all of a sub-chunk's words
+    // can be in flight from the start without one wave stalling on their issue.
+    // Streams above 0 hand their block sums and scales to stream 0 through LDS,
+    // which folds them into acc in block order: the summation order (and so the
+    // result) does not depend on KW.
+    // (Four waves per tile measured slower: a 1024-thread workgroup leaves too
+    // few resident per CU.)
+    static_assert(KW == 1 || KW == 2, "one or two waves per row tile");
+    static_assert(C % KW == 0, "each wave stream takes whole blocks");
+    constexpr int NT = kThreads * KW;
+    constexpr int CB = C / KW;
     __shared__ float lut[BT][C][kLutFloats];
+    __shared__ float2 xchg[KW > 1 ? (KW - 1) * CB * BT : 1][kThreads];
     __shared__ unsigned s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int tile = blockIdx.x * (kThreads / kTileRows) + (tid >> 6);
+    const int stream = __builtin_amdgcn_readfirstlane(tid / kThreads);  // wave-uniform, branched on as such
+    const int tile = blockIdx.x * (kThreads / kTileRows) + ((tid & (kThreads - 1)) >> 6);
     const int row = tile * kTileRows + lane;
-    const bool row_ok = row < N;
+    const bool row_ok = row < N && stream == 0;  // lanes that hold and write the result
     const int b0 = blockIdx.y * BT;
     const int g_begin = blockIdx.z * chunk_groups;
     const int g_end = g_begin + chunk_groups;
@@ -499,66 +520,100 @@ __global__ __launch_bounds__(kThreads) void lut_gemv_kernel(
 #pragma unroll
     for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
 
-    for (int g0 = g_begin; g0 < g_end; g0 += C) {
-        // 1. Activations for this thread's table tasks, then this row's C blocks:
-        //    the whole weight chunk is in flight while the tables are built.
-        T xv[lut_task_iters(C, BT)][3];
-        load_lut_inputs<T, C, BT>(xv, x, K, M, b0, g0, tid);
-        // Only the first kLutLoadAhead blocks' words are issued here; block
-        // c + kLutLoadAhead is issued as block c is consumed. A wave that
-        // issued all of its loads at once would stall on issue while the CU's
-        // memory queue drains, and reach its first sum only then.
-        uint32_t w[C][kBlockWords];
+    // The work of one wave stream (a compile-time block range, so every table
+    // and word offset stays an immediate). Per sub-chunk of C groups:
+    //   1. the activations of this thread's table tasks, then this row's
+    //      blocks: only the first kLutLoadAhead blocks' words are issued before
+    //      the tables, block c + kLutLoadAhead as block c is consumed -- a wave
+    //      that issued all of its loads at once would stall on issue while the
+    //      CU's memory queue drains, and reach its first sum only then;
+    //   2. the tables, after every lane is done reading the previous ones;
+    //   3. the blocks, in load order (loads complete in order; rows past N
+    //      compute a discarded value). Within a block: slot 0..24, the tail,
+    //      then one fma with the scale; blocks fold into acc in order -- the
+    //      reference's summation order. Streams above 0 leave their block sums
+    //      and scales in LDS; stream 0 folds them after a barrier.
+    using XV = T[lut_task_iters(C, BT, NT)][3];
+    auto run = [&](auto stream_tag, const XV &xv, int g0) {
+        constexpr int cb0 = decltype(stream_tag)::value * CB;
         const uint32_t *wp = row_words + static_cast<int64_t>(g0) * kTileGroupWords;
+        uint32_t w[CB][kBlockWords];
 #pragma unroll
-        for (int c = 0; c < (kLutLoadAhead < C ? kLutLoadAhead : C); ++c)
+        for (int c = 0; c < (kLutLoadAhead < CB ? kLutLoadAhead : CB); ++c)
 #pragma unroll
-            for (int j = 0; j < kBlockWords; ++j) w[c][j] = wp[(c * kBlockWords + j) * kTileRows];
+            for (int j = 0; j < kBlockWords; ++j) w[c][j] = wp[((cb0 + c) * kBlockWords + j) * kTileRows];
         __builtin_amdgcn_sched_barrier(0);
-
-        // 2. Tables (after every lane is done reading the previous ones).
-        if (g0 != g_begin) __syncthreads();
-        build_lut_tables<T, C, BT>(lut, xv, tid);
-        __syncthreads();
-
-        // 3. Consume (rows past N compute a discarded value), block by block in
-        //    load order, so block c is summed while blocks c+1.. are still
-        //    arriving (loads complete in order). Within a block: slot 0..24,
-        //    the tail, then one fma with the scale; blocks fold into acc in
-        //    order -- the reference's summation order.
+        {
+            // (With several streams the fold barrier below already orders the
+            // previous sub-chunk's table and exchange reads before this.)
+            if (KW == 1 && g0 != g_begin) __syncthreads();
+            build_lut_tables<T, C, BT, NT>(lut, xv, tid);
+            __syncthreads();
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-            if (c + kLutLoadAhead < C) {
+            for (int c = 0; c < CB; ++c) {
+                if (c + kLutLoadAhead < CB) {
 #pragma unroll
-                for (int j = 0; j < kBlockWords; ++j)
-                    w[c + kLutLoadAhead][j] = wp[((c + kLutLoadAhead) * kBlockWords + j) * kTileRows];
+                    for (int j = 0; j < kBlockWords; ++j)
+                        w[c + kLutLoadAhead][j] = wp[((cb0 + c + kLutLoadAhead) * kBlockWords + j) * kTileRows];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // The sum starts at slot 0's pair rather than at 0 + pair:
+                // equal except that a -0 pair stays -0, which the fma into acc
+                // (from +0) turns into the same +0.
+                float sum[BT];
+#pragma unroll
+                for (int word = 0; word < kBlockWords; ++word) {
+                    uint32_t lo[4], hi[4];
+                    split_word(w[c][word], lo, hi);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
+                        if (s < 0 || s >= kFullSlots) continue;
+#pragma unroll
+                        for (int j = 0; j < BT; ++j) {
+                            const float pair = lut[j][cb0 + c][s * kL2Entries + lo[b]] +
+                                               lut[j][cb0 + c][kL3Base + s * kL3Entries + hi[b]];
+                            sum[j] = s == 0 ? pair : sum[j] + pair;
+                        }
+                    }
+                }
+                const float scale = half_bits_to_float(w[c][0]);
+                const uint32_t tail = min(w[c][6] >> 24, kMaxTailByte);
+#pragma unroll
+                for (int j = 0; j < BT; ++j) {
+                    sum[j] += lut[j][cb0 + c][kTailBase + tail];
+                    if constexpr (cb0 == 0)
+                        acc[j] = fmaf(scale, sum[j], acc[j]);
+                    else
+                        xchg[((cb0 - CB) + c) * BT + j][tid & (kThreads - 1)] = make_float2(sum[j], scale);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            float sum[BT];
+            if constexpr (KW > 1) {
+                __syncthreads();
+                if constexpr (cb0 == 0) {
 #pragma unroll
-            for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
+                    for (int c = 0; c < (KW - 1) * CB; ++c)
 #pragma unroll
-            for (int word = 0; word < kBlockWords; ++word) {
-                uint32_t lo[4], hi[4];
-                split_word(w[c][word], lo, hi);
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
-                    if (s < 0 || s >= kFullSlots) continue;
-#pragma unroll
-                    for (int j = 0; j < BT; ++j)
-                        sum[j] += lut[j][c][s * kL2Entries + lo[b]] + lut[j][c][kL3Base + s * kL3Entries + hi[b]];
+                        for (int j = 0; j < BT; ++j) {
+                            const float2 v = xchg[c * BT + j][tid];
+                            acc[j] = fmaf(v.y, v.x, acc[j]);
+                        }
                 }
             }
-            const float scale = half_bits_to_float(w[c][0]);
-            const uint32_t tail = min(w[c][6] >> 24, kMaxTailByte);
-#pragma unroll
-            for (int j = 0; j < BT; ++j) {
-                sum[j] += lut[j][c][kTailBase + tail];
-                acc[j] = fmaf(scale, sum[j], acc[j]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    for (int g0 = g_begin; g0 < g_end; g0 += C) {
+        // Activations first, outside the per-stream code: loaded there, the
+        // compiler sinks the third activation of each task into the table
+        // build's L3 branch, behind the word loads, and the build then waits
+        // for every word.
+        XV xv;
+        load_lut_inputs<T, C, BT, NT>(xv, x, K, M, b0, g0, tid);
+        if (KW == 1 || stream == 0)
+            run(std::integral_constant<int, 0>{}, xv, g0);
+        else if constexpr (KW == 2)
+            run(std::integral_constant<int, 1>{}, xv, g0);
     }
 
     // 4. Output. With GLU, rows 2r and 2r+1 are the gate and up rows of one
@@ -1698,6 +1753,7 @@ constexpr size_t kCounterRegionBytes = kCounterSlots * sizeof(unsigned);
 
 struct LutPlan {
     int batch_tile;
+    int waves;         // waves per 64-row tile (compile-time KW)
     int chunk;         // groups per sub-chunk (compile-time C)
     int chunk_groups;  // groups per workgroup, a multiple of chunk
     int k_split;
@@ -1712,6 +1768,8 @@ bool lut_chunk_supported(int batch_tile, int chunk) {
     return chunk == 1 || chunk == 2 || chunk == 4 || chunk == 8;
 }
 
+int device_cu_count();  // the current device's CUs (256 when it cannot be queried)
+
 int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split, LutPlan *plan) {
     const int64_t G = columns / kBlockWeights;
     // Measured on MI355X: one vector per workgroup beats batch tiles of 2 and 4
@@ -1721,6 +1779,7 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
     if (batch_tile != 1 && batch_tile != 2 && batch_tile != 4)
         return fail(TERNEL_TQ1_EINVAL, "batch tile must be 1, 2 or 4, got %d", batch_tile);
     plan->batch_tile = batch_tile;
+    plan->waves = 1;
     plan->row_blocks = ceil_div(rows, kThreads);
     plan->batch_tiles = ceil_div(M, batch_tile);
     if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
@@ -1758,6 +1817,17 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
         plan->chunk_groups = c;
         plan->k_split = static_cast<int>(G / c);
     }
+    // Two waves per row tile, each summing half of a sub-chunk's blocks, for
+    // one vector per workgroup: a wave's blocks are all in flight before its
+    // first sum. That pays while the grid is resident at once (three 512-thread
+    // workgroups per CU) or a chunk has eight blocks; a longer grid streams
+    // better with single-wave tiles. Measured on MI355X (graph-replayed, cold,
+    // us, one wave -> two): M=1 down 12.4 -> 11.0, QKV 8.4 -> 8.0, gate/up
+    // 9.9 -> 9.8; M=2 down 14.7 -> 14.0 but gate/up 13.6 -> 14.3; the 248320-row
+    // head 62.6 -> 75.7.
+    if (plan->batch_tile == 1 && plan->chunk >= 2 &&
+        (plan->chunk >= 8 || plan->row_blocks * plan->batch_tiles * plan->k_split <= 3 * device_cu_count()))
+        plan->waves = 2;
     if (plan->k_split > 65535) return fail(TERNEL_TQ1_EINVAL, "K too large for one launch");
     if (plan->k_split > 1 && plan->row_blocks * plan->batch_tiles > kCounterSlots)
         return fail(TERNEL_TQ1_EINVAL, "%lld row blocks x %lld batch tiles exceed the %d split-K counters",
@@ -1774,6 +1844,14 @@ void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *
                        unsigned *counters, int64_t M, int64_t rows, int G, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.batch_tiles),
                     static_cast<unsigned>(plan.k_split));
+    if constexpr (BT == 1 && C >= 2) {
+        if (plan.waves == 2) {
+            hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU, 2>), grid, dim3(2 * kThreads), 0, stream, packed,
+                               static_cast<const T *>(x), static_cast<T *>(y), partial, counters,
+                               static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
+            return;
+        }
+    }
     hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU>), grid, dim3(kThreads), 0, stream, packed,
                        static_cast<const T *>(x), static_cast<T *>(y), partial, counters, static_cast<int>(M),
                        static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);

@@ -62,7 +62,9 @@ def test_every_fp16_scale_pattern_reaches_the_output() -> None:
     np.testing.assert_array_equal(got[np.isinf(want)], want[np.isinf(want)])
 
 
-SHAPES = ((48, 5120), (256, 640), (512, 384), (1024, 5120), (300, 256))
+# 1536 and 2560 columns (12 and 20 groups) run as 4-group sub-chunks with the
+# next one's loads issued early, including an odd last sub-chunk.
+SHAPES = ((48, 5120), (256, 640), (512, 384), (1024, 5120), (300, 256), (256, 1536), (320, 2560))
 
 
 @pytest.mark.parametrize(("rows", "columns"), SHAPES)
