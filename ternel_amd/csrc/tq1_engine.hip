@@ -607,9 +607,13 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         // Activations first, outside the per-stream code: loaded there, the
         // compiler sinks the third activation of each task into the table
         // build's L3 branch, behind the word loads, and the build then waits
-        // for every word.
+        // for every word. They are also waited for before any word is issued:
+        // behind the chip-wide burst of word loads an activation load takes
+        // longer than the wait (measured gate/up 9.84 -> 9.70 us, QKV 8.01 ->
+        // 7.82).
         XV xv;
         load_lut_inputs<T, C, BT, NT>(xv, x, K, M, b0, g0, tid);
+        wait_vector_memory();
         if (KW == 1 || stream == 0)
             run(std::integral_constant<int, 0>{}, xv, g0);
         else if constexpr (KW == 2)
@@ -1243,11 +1247,27 @@ __device__ __forceinline__ int wide_owner(int units, int u, int P) {
 // Activations in the direct forms' K order: within every group, 4-half unit u
 // of the copy is unit direct_source_unit(u) of x, so that the wide kernel can
 // stage 16-byte runs with LDS-DMA.
+// A thread writes four consecutive units of the copy (two 16-byte stores when
+// the copy is 16-byte aligned): a quarter of the threads and half of the store
+// instructions of a unit-per-thread copy.
 __global__ __launch_bounds__(kThreads) void permute_activations_kernel(const uint2 *__restrict__ x,
-                                                                      uint2 *__restrict__ xp, int64_t units) {
+                                                                      uint2 *__restrict__ xp, int64_t quads,
+                                                                      int wide_stores) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= units) return;
-    xp[i] = x[(i & ~int64_t(31)) + direct_source_unit(static_cast<int>(i & 31))];
+    if (i >= quads) return;
+    const int64_t base = (i >> 3) * 32;  // the group's first unit
+    const int u0 = static_cast<int>(i & 7) * 4;
+    uint2 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = x[base + direct_source_unit(u0 + k)];
+    if (wide_stores) {
+        uint4 *dst = reinterpret_cast<uint4 *>(xp + base + u0);
+        dst[0] = uint4{v[0].x, v[0].y, v[1].x, v[1].y};
+        dst[1] = uint4{v[2].x, v[2].y, v[3].x, v[3].y};
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xp[base + u0 + k] = v[k];
+    }
 }
 
 // Uses every decoded dword in an empty asm statement, so the decode of a
@@ -1601,32 +1621,62 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             }
         }
         __syncthreads();
+        // The sum runs in workgroup order q0..q1: the partials of q0..p-1, this
+        // workgroup's accumulators, then the partials of p+1..q1. It is formed
+        // in place in acc -- (prefix) + acc equals acc + (prefix) exactly in
+        // fp32 -- in batches of kRB fragments whose loads are all in flight at
+        // once: the reduction at the end of a launch costs one memory round
+        // trip per batch and contributor, not one per fragment (batches of two
+        // for eight-block tiles, whose accumulators leave no more registers).
+        constexpr int kRB = NB == 8 ? 2 : (NB < 4 ? NB : 4);
+        auto load_batch = [&](float (&v)[kRB][16], int q, int nb0) {
+            // The tile is contributor q's first segment unless q starts before it.
+            const int base = slot_base(q, wide_unit_begin(geo.units, q, P) >= tu0 ? 0 : 1);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            float sum[16];
-            for (int q = q0; q <= q1; ++q) {
-                float v[16];
-                if (q == p) {
+            for (int i = 0; i < kRB; ++i)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) v[e] = acc[nb][e];
-                } else {
-                    // The tile is contributor q's first segment unless q starts before it.
-                    const int base = slot_base(q, wide_unit_begin(geo.units, q, P) >= tu0 ? 0 : 1);
+                for (int r = 0; r < 4; ++r) {
+                    const f32x4 f = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, voff_p, base + ((nb0 + i) * 4 + r) * 1024,
+                                                                      kDeviceCoherent));
+                    v[i][4 * r] = f.x;
+                    v[i][4 * r + 1] = f.y;
+                    v[i][4 * r + 2] = f.z;
+                    v[i][4 * r + 3] = f.w;
+                }
+        };
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const f32x4 f = __builtin_bit_cast(
-                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, voff_p, base + (nb * 4 + r) * 1024,
-                                                                          kDeviceCoherent));
-                        v[4 * r] = f.x;
-                        v[4 * r + 1] = f.y;
-                        v[4 * r + 2] = f.z;
-                        v[4 * r + 3] = f.w;
-                    }
+        for (int nb0 = 0; nb0 < NB; nb0 += kRB) {
+            float v[kRB][16];
+            if (p > q0) {
+                load_batch(v, q0, nb0);
+                for (int q = q0 + 1; q < p; ++q) {
+                    float w2[kRB][16];
+                    load_batch(w2, q, nb0);
+#pragma unroll
+                    for (int i = 0; i < kRB; ++i)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) v[i][e] += w2[i][e];
                 }
 #pragma unroll
-                for (int e = 0; e < 16; ++e) sum[e] = q == q0 ? v[e] : sum[e] + v[e];
+                for (int i = 0; i < kRB; ++i)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[nb0 + i][e] = v[i][e] + acc[nb0 + i][e];
             }
-            store_frag(t, nb, sum);
+            for (int q = p + 1; q <= q1; ++q) {
+                load_batch(v, q, nb0);
+#pragma unroll
+                for (int i = 0; i < kRB; ++i)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[nb0 + i][e] += v[i][e];
+            }
+#pragma unroll
+            for (int i = 0; i < kRB; ++i) {
+                float out[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) out[e] = acc[nb0 + i][e];
+                store_frag(t, nb0 + i, out);
+            }
         }
         if (tid == 0) {
             __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2135,9 +2185,10 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
     unsigned *counters = static_cast<unsigned *>(ws);
     float *partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes);
     _Float16 *xp = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kCounterRegionBytes + plan.partial_bytes);
-    const int64_t units = static_cast<int64_t>(plan.geo.M) * plan.geo.G * 32;  // 8-byte units of x
-    hipLaunchKernelGGL(permute_activations_kernel, dim3(static_cast<unsigned>(ceil_div(units, kThreads))),
-                       dim3(kThreads), 0, stream, static_cast<const uint2 *>(x), reinterpret_cast<uint2 *>(xp), units);
+    const int64_t quads = static_cast<int64_t>(plan.geo.M) * plan.geo.G * 8;  // 32-byte runs of the copy
+    hipLaunchKernelGGL(permute_activations_kernel, dim3(static_cast<unsigned>(ceil_div(quads, kThreads))),
+                       dim3(kThreads), 0, stream, static_cast<const uint2 *>(x), reinterpret_cast<uint2 *>(xp), quads,
+                       static_cast<int>(reinterpret_cast<uintptr_t>(xp) % 16 == 0));
     TQ1_LAUNCH_CHECK();
     WideGeometry geo = plan.geo;
     geo.vector_rows = geo.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
