@@ -383,6 +383,19 @@ __device__ __forceinline__ void load_lut_inputs(T (&xv)[lut_task_iters(C, BT, NT
     }
 }
 
+// Uses every loaded activation in an empty asm statement placed after the
+// wait for them: none of the loads can then be sunk behind later ones (the
+// compiler would otherwise move the third activation of a task into the table
+// build's L3 branch, behind the word loads).
+template <typename T, int N>
+__device__ __forceinline__ void pin_loaded(const T (&xv)[N][3]) {
+    using Bits = std::conditional_t<sizeof(T) == 2, uint16_t, uint32_t>;
+#pragma unroll
+    for (int it = 0; it < N; ++it)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) asm volatile("" ::"v"(__builtin_bit_cast(Bits, xv[it][k])));
+}
+
 template <typename T, int C, int BT, int NT>
 __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
                                                  const T (&xv)[lut_task_iters(C, BT, NT)][3], int tid) {
@@ -417,29 +430,40 @@ __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
 
 // LUT23 split of the 25 code bytes of a block, two bytes per 16-bit-packed
 // operation: hi = (p * 57) >> 9 == p / 9 (exact for p <= 511), lo = p - 9 hi.
+// Each 16-bit digit becomes a table byte address with one multiply-add that
+// selects its half (v_mad_u32_u16 with op_sel): 4 * digit + base, where base is
+// the wave's table base; slot and block offsets go in the reads' immediates.
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ void split_pair(uint32_t pair, uint32_t &lo_a, uint32_t &hi_a, uint32_t &lo_b,
-                                           uint32_t &hi_b) {
-    u16x2 p = __builtin_bit_cast(u16x2, pair);
-    u16x2 h = (p * static_cast<unsigned short>(57)) >> static_cast<unsigned short>(9);
-    const u16x2 l = p - h * static_cast<unsigned short>(9);
-    // Hide h's range (< 32) from the compiler: with it known, the low half is
-    // unpacked as (h & 31) << 2, two instructions, instead of one SDWA shift.
-    uint32_t hb = __builtin_bit_cast(uint32_t, h);
-    asm volatile("" : "+v"(hb));
-    h = __builtin_bit_cast(u16x2, hb);
-    lo_a = l.x;
-    hi_a = h.x;
-    lo_b = l.y;
-    hi_b = h.y;
+__device__ __forceinline__ uint32_t lut_address_lo(uint32_t pair, uint32_t base) {
+    uint32_t r;
+    asm("v_mad_u32_u16 %0, %1, 4, %2" : "=v"(r) : "v"(pair), "v"(base));
+    return r;
+}
+__device__ __forceinline__ uint32_t lut_address_hi(uint32_t pair, uint32_t base) {
+    uint32_t r;
+    asm("v_mad_u32_u16 %0, %1, 4, %2 op_sel:[1,0,0,0]" : "=v"(r) : "v"(pair), "v"(base));
+    return r;
 }
 
-// All four bytes of a block word: lo/hi for byte b of the word. Bytes 1 and 3
-// move to the 16-bit halves with one byte permute (selector 0x0c = zero).
-__device__ __forceinline__ void split_word(uint32_t word, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
-    split_pair(word & 0x00ff00ffu, lo[0], hi[0], lo[2], hi[2]);                           // bytes 0 and 2
-    split_pair(__builtin_amdgcn_perm(0u, word, 0x0c030c01u), lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
+__device__ __forceinline__ void split_pair(uint32_t pair, uint32_t base, uint32_t &lo_a, uint32_t &hi_a,
+                                           uint32_t &lo_b, uint32_t &hi_b) {
+    const u16x2 p = __builtin_bit_cast(u16x2, pair);
+    const u16x2 h = (p * static_cast<unsigned short>(57)) >> static_cast<unsigned short>(9);
+    const u16x2 l = p - h * static_cast<unsigned short>(9);
+    const uint32_t hb = __builtin_bit_cast(uint32_t, h), lb = __builtin_bit_cast(uint32_t, l);
+    lo_a = lut_address_lo(lb, base);
+    hi_a = lut_address_lo(hb, base);
+    lo_b = lut_address_hi(lb, base);
+    hi_b = lut_address_hi(hb, base);
+}
+
+// All four bytes of a block word: table byte addresses lo/hi for byte b of the
+// word. Bytes 1 and 3 move to the 16-bit halves with one byte permute
+// (selector 0x0c = zero).
+__device__ __forceinline__ void split_word(uint32_t word, uint32_t base, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+    split_pair(word & 0x00ff00ffu, base, lo[0], hi[0], lo[2], hi[2]);                           // bytes 0 and 2
+    split_pair(__builtin_amdgcn_perm(0u, word, 0x0c030c01u), base, lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
 }
 
 // Adds partial[0..k) (stride apart) left to right. The agent-coherent loads of
@@ -520,8 +544,11 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
 #pragma unroll
     for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
 
-    // The work of one wave stream (a compile-time block range, so every table
-    // and word offset stays an immediate). Per sub-chunk of C groups:
+    // The work of one wave stream -- blocks [stream * CB, (stream + 1) * CB) of
+    // every sub-chunk. One copy of the code serves every stream, whose word
+    // loads and table reads start from its own base: a copy per stream (table
+    // offsets as immediates) doubled the code for the same speed. Per sub-chunk
+    // of C groups:
     //   1. the activations of this thread's table tasks, then this row's
     //      blocks: only the first kLutLoadAhead blocks' words are issued before
     //      the tables, block c + kLutLoadAhead as block c is consumed -- a wave
@@ -534,90 +561,87 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     //      reference's summation order. Streams above 0 leave their block sums
     //      and scales in LDS; stream 0 folds them after a barrier.
     using XV = T[lut_task_iters(C, BT, NT)][3];
-    auto run = [&](auto stream_tag, const XV &xv, int g0) {
-        constexpr int cb0 = decltype(stream_tag)::value * CB;
-        const uint32_t *wp = row_words + static_cast<int64_t>(g0) * kTileGroupWords;
+    const int cb0 = stream * CB;  // first block of this wave's stream
+    const char *const lut_bytes = reinterpret_cast<const char *>(&lut[0][0][0]);
+    const uint32_t lut_base = static_cast<uint32_t>(cb0 * kLutFloats * 4);
+    auto table = [&](uint32_t address, int j, int c, int entry) {
+        return *reinterpret_cast<const float *>(lut_bytes + address + ((j * C + c) * kLutFloats + entry) * 4);
+    };
+    auto run = [&](const XV &xv, int g0) {
+        const uint32_t *wp = row_words + (static_cast<int64_t>(g0) * kBlockWords + cb0 * kBlockWords) * kTileRows;
         uint32_t w[CB][kBlockWords];
 #pragma unroll
         for (int c = 0; c < (kLutLoadAhead < CB ? kLutLoadAhead : CB); ++c)
 #pragma unroll
-            for (int j = 0; j < kBlockWords; ++j) w[c][j] = wp[((cb0 + c) * kBlockWords + j) * kTileRows];
+            for (int j = 0; j < kBlockWords; ++j) w[c][j] = wp[(c * kBlockWords + j) * kTileRows];
         __builtin_amdgcn_sched_barrier(0);
-        {
-            // (With several streams the fold barrier below already orders the
-            // previous sub-chunk's table and exchange reads before this.)
-            if (KW == 1 && g0 != g_begin) __syncthreads();
-            build_lut_tables<T, C, BT, NT>(lut, xv, tid);
-            __syncthreads();
+        // (With several streams the fold barrier below already orders the
+        // previous sub-chunk's table and exchange reads before this.)
+        if (KW == 1 && g0 != g_begin) __syncthreads();
+        build_lut_tables<T, C, BT, NT>(lut, xv, tid);
+        __syncthreads();
 #pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                if (c + kLutLoadAhead < CB) {
+        for (int c = 0; c < CB; ++c) {
+            if (c + kLutLoadAhead < CB) {
 #pragma unroll
-                    for (int j = 0; j < kBlockWords; ++j)
-                        w[c + kLutLoadAhead][j] = wp[((cb0 + c + kLutLoadAhead) * kBlockWords + j) * kTileRows];
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                // The sum starts at slot 0's pair rather than at 0 + pair:
-                // equal except that a -0 pair stays -0, which the fma into acc
-                // (from +0) turns into the same +0.
-                float sum[BT];
+                for (int j = 0; j < kBlockWords; ++j)
+                    w[c + kLutLoadAhead][j] = wp[((c + kLutLoadAhead) * kBlockWords + j) * kTileRows];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // The sum starts at slot 0's pair rather than at 0 + pair: equal
+            // except that a -0 pair stays -0, which the fma into acc (from +0)
+            // turns into the same +0.
+            float sum[BT];
 #pragma unroll
-                for (int word = 0; word < kBlockWords; ++word) {
-                    uint32_t lo[4], hi[4];
-                    split_word(w[c][word], lo, hi);
+            for (int word = 0; word < kBlockWords; ++word) {
+                uint32_t lo[4], hi[4];
+                split_word(w[c][word], lut_base, lo, hi);
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
-                        if (s < 0 || s >= kFullSlots) continue;
+                for (int b = 0; b < 4; ++b) {
+                    const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
+                    if (s < 0 || s >= kFullSlots) continue;
 #pragma unroll
-                        for (int j = 0; j < BT; ++j) {
-                            const float pair = lut[j][cb0 + c][s * kL2Entries + lo[b]] +
-                                               lut[j][cb0 + c][kL3Base + s * kL3Entries + hi[b]];
-                            sum[j] = s == 0 ? pair : sum[j] + pair;
-                        }
+                    for (int j = 0; j < BT; ++j) {
+                        const float pair =
+                            table(lo[b], j, c, s * kL2Entries) + table(hi[b], j, c, kL3Base + s * kL3Entries);
+                        sum[j] = s == 0 ? pair : sum[j] + pair;
                     }
                 }
-                const float scale = half_bits_to_float(w[c][0]);
-                const uint32_t tail = min(w[c][6] >> 24, kMaxTailByte);
-#pragma unroll
-                for (int j = 0; j < BT; ++j) {
-                    sum[j] += lut[j][cb0 + c][kTailBase + tail];
-                    if constexpr (cb0 == 0)
-                        acc[j] = fmaf(scale, sum[j], acc[j]);
-                    else
-                        xchg[((cb0 - CB) + c) * BT + j][tid & (kThreads - 1)] = make_float2(sum[j], scale);
-                }
-                __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (KW > 1) {
-                __syncthreads();
-                if constexpr (cb0 == 0) {
+            const float scale = half_bits_to_float(w[c][0]);
+            const uint32_t tail = lut_base + 4 * min(w[c][6] >> 24, kMaxTailByte);
 #pragma unroll
-                    for (int c = 0; c < (KW - 1) * CB; ++c)
+            for (int j = 0; j < BT; ++j) {
+                sum[j] += table(tail, j, c, kTailBase);
+                if (KW == 1 || stream == 0)
+                    acc[j] = fmaf(scale, sum[j], acc[j]);
+                else
+                    xchg[((stream - 1) * CB + c) * BT + j][tid & (kThreads - 1)] = make_float2(sum[j], scale);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (KW > 1) {
+            __syncthreads();
+            if (stream == 0) {
 #pragma unroll
-                        for (int j = 0; j < BT; ++j) {
-                            const float2 v = xchg[c * BT + j][tid];
-                            acc[j] = fmaf(v.y, v.x, acc[j]);
-                        }
-                }
+                for (int c = 0; c < (KW - 1) * CB; ++c)
+#pragma unroll
+                    for (int j = 0; j < BT; ++j) {
+                        const float2 v = xchg[c * BT + j][tid];
+                        acc[j] = fmaf(v.y, v.x, acc[j]);
+                    }
             }
         }
     };
     for (int g0 = g_begin; g0 < g_end; g0 += C) {
-        // Activations first, outside the per-stream code: loaded there, the
-        // compiler sinks the third activation of each task into the table
-        // build's L3 branch, behind the word loads, and the build then waits
-        // for every word. They are also waited for before any word is issued:
-        // behind the chip-wide burst of word loads an activation load takes
-        // longer than the wait (measured gate/up 9.84 -> 9.70 us, QKV 8.01 ->
-        // 7.82).
+        // Activations first, waited for before any word is issued: behind the
+        // chip-wide burst of word loads an activation load takes longer than
+        // the wait (measured gate/up 9.84 -> 9.70 us, QKV 8.01 -> 7.82).
         XV xv;
         load_lut_inputs<T, C, BT, NT>(xv, x, K, M, b0, g0, tid);
         wait_vector_memory();
-        if (KW == 1 || stream == 0)
-            run(std::integral_constant<int, 0>{}, xv, g0);
-        else if constexpr (KW == 2)
-            run(std::integral_constant<int, 1>{}, xv, g0);
+        pin_loaded(xv);
+        run(xv, g0);
     }
 
     // 4. Output. With GLU, rows 2r and 2r+1 are the gate and up rows of one
