@@ -198,11 +198,11 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
  * two unfused layers would return them, and SiLU(g) * u is computed in fp32.
  * z is [M][rows / 2] in the activation type. No counterpart in the reference
  * (its MLP runs gate_proj, up_proj and the activation as separate mlx ops,
- * src/ternel_mlx/packed_model.py:72-92); this is the fused-MLP epilogue of its
- * scope table's next rows. Batches up to 4 (and bf16/fp32 activations) run the
- * LUT23 kernel with the pair exchange in its epilogue; larger fp16 batches run
- * the GEMM into the workspace and one elementwise pass. Workspace from
- * ternel_tq1_swiglu_workspace_bytes, same contract as ternel_tq1_linear's.
+ * src/ternel_mlx/packed_model.py:72-92). Batches that ternel_tq1_linear sends
+ * to the LUT23 kernel (up to 4 rows, 6 for matrices under 16 MiB, and every
+ * bf16/fp32 batch) run it with the pair exchange in its epilogue; larger fp16
+ * batches run the GEMM into the workspace and one elementwise pass. Workspace
+ * from ternel_tq1_swiglu_workspace_bytes, same contract as ternel_tq1_linear's.
  */
 int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M, int64_t rows, int64_t columns,
                       int dtype, void *ws, size_t ws_bytes, void *stream);
