@@ -357,6 +357,13 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
 // in-order vmcnt wait of the build never waits behind the weight stream.
 // Blocks whose words are in flight ahead of the one being consumed.
 constexpr int kLutLoadAhead = 2;
+// Offset in the group of table task k's first activation; its second is the
+// next one, its third the one after that (L3 slots and the tail; L2 slots
+// repeat the second).
+__device__ __forceinline__ int lut_task_base(int k) {
+    return k < kFullSlots ? 5 * k : (k < 2 * kFullSlots ? 5 * (k - kFullSlots) + 2 : 125);
+}
+
 constexpr int lut_task_count(int c, int bt) { return bt * c * kTasksPerGroup; }
 constexpr int lut_task_iters(int c, int bt, int threads) { return (lut_task_count(c, bt) + threads - 1) / threads; }
 
@@ -374,9 +381,8 @@ __device__ __forceinline__ void load_lut_inputs(T (&xv)[lut_task_iters(C, BT, NT
         const int k = rem - c * kTasksPerGroup;
         const int sample = min(b0 + j, M - 1);
         const T *xg = x + static_cast<int64_t>(sample) * K + static_cast<int64_t>(g0 + c) * kBlockWeights;
-        // L2 task k < 25: x[5k], x[5k+1]; L3 task: x[5s+2..5s+4]; tail: x[125..127].
         // Kept raw: converting here would make the loads wait before the weight loads issue.
-        const int base = k < kFullSlots ? 5 * k : (k < 2 * kFullSlots ? 5 * (k - kFullSlots) + 2 : 125);
+        const int base = lut_task_base(k);
         xv[it][0] = xg[base];
         xv[it][1] = xg[base + 1];
         xv[it][2] = xg[k < kFullSlots ? base + 1 : base + 2];
@@ -396,6 +402,30 @@ __device__ __forceinline__ void pin_loaded(const T (&xv)[N][3]) {
         for (int k = 0; k < 3; ++k) asm volatile("" ::"v"(__builtin_bit_cast(Bits, xv[it][k])));
 }
 
+// Table task k of one group (k < 25: L2 slot k from x[5k], x[5k+1]; k < 50:
+// L3 slot k - 25 from x[5s+2..5s+4]; k = 50: the tail from x[125..127]), the
+// activations x0..x2 raw. Entries are (t - 1) * x as real products, so
+// 0 * inf = NaN propagates as in the reference.
+template <typename T>
+__device__ __forceinline__ void write_lut_task(float *L, int k, T xr0, T xr1, T xr2) {
+    const float x0 = to_f32<T>(xr0);
+    const float x1 = to_f32<T>(xr1);
+    const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
+    const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
+    if (k < kFullSlots) {
+        float *dst = L + k * kL2Entries;
+#pragma unroll
+        for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
+    } else {
+        const float x2 = to_f32<T>(xr2);
+        const float d[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
+        const int s = k - kFullSlots;
+        float *dst = L + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
+#pragma unroll
+        for (int e = 0; e < kL3Entries; ++e) dst[e] = (a[e % 3] + b[(e / 3) % 3]) + d[e / 9];
+    }
+}
+
 template <typename T, int C, int BT, int NT>
 __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
                                                  const T (&xv)[lut_task_iters(C, BT, NT)][3], int tid) {
@@ -407,24 +437,7 @@ __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
         const int rem = task - j * (C * kTasksPerGroup);
         const int c = rem / kTasksPerGroup;
         const int k = rem - c * kTasksPerGroup;
-        float *L = lut[j][c];
-        const float x0 = to_f32<T>(xv[it][0]);
-        const float x1 = to_f32<T>(xv[it][1]);
-        // (t - 1) * x as real products, so 0 * inf = NaN propagates as in the reference.
-        const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
-        const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
-        if (k < kFullSlots) {
-            float *dst = L + k * kL2Entries;
-#pragma unroll
-            for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
-        } else {
-            const float x2 = to_f32<T>(xv[it][2]);
-            const float d[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
-            const int s = k - kFullSlots;
-            float *dst = L + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
-#pragma unroll
-            for (int e = 0; e < kL3Entries; ++e) dst[e] = (a[e % 3] + b[(e / 3) % 3]) + d[e / 9];
-        }
+        write_lut_task<T>(lut[j][c], k, xv[it][0], xv[it][1], xv[it][2]);
     }
 }
 

@@ -192,7 +192,10 @@ def test_auto_configuration_meets_the_north_star_tolerance(batch: int) -> None:
 # One vector with the split left automatic (the M = 1 decode path): K chunks
 # of four or eight groups reduced in chunk order. The shapes cover a single
 # group (no split), ragged rows, and K from 2 to 136 groups.
-AUTO_SHAPES = ((128, 128), (64, 256), (300, 640), (8192, 1024), (2048, 5120), (1024, 17408), (4096, 2048))
+# Ragged row counts (4000 = 62.5 64-row tiles, 26240 rows of 5 groups) and the
+# QKV shape among them.
+AUTO_SHAPES = ((128, 128), (64, 256), (300, 640), (8192, 1024), (2048, 5120), (1024, 17408), (4096, 2048),
+               (4096, 4096), (4000, 5120), (26240, 640), (8192, 5120))
 
 
 def run_auto(blocks: np.ndarray, x: np.ndarray, dtype=torch.float32) -> torch.Tensor:
@@ -237,17 +240,19 @@ def test_auto_split_gemv_of_one_group_is_bit_exact_against_the_lut23_oracle() ->
                                   O.lut23_matmul(blocks, x, rows=200, columns=128))
 
 
-def test_auto_split_gemv_is_bit_identical_between_runs() -> None:
-    blocks = random_blocks(2048, 17408, seed=77)
-    x = np.random.default_rng(77).normal(0.0, 1.0, size=(1, 17408)).astype(np.float32)
+@pytest.mark.parametrize(("rows", "columns"), ((2048, 17408), (4000, 5120)))
+def test_auto_split_gemv_is_bit_identical_between_runs(rows: int, columns: int) -> None:
+    blocks = random_blocks(rows, columns, seed=77)
+    x = np.random.default_rng(77).normal(0.0, 1.0, size=(1, columns)).astype(np.float32)
     first = run_auto(blocks, x).cpu().numpy()
     for _ in range(3):
         np.testing.assert_array_equal(run_auto(blocks, x).cpu().numpy(), first)
 
 
+@pytest.mark.parametrize("rows", (1024, 4000))
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
-def test_auto_split_gemv_rounds_once_at_the_store(dtype) -> None:
-    blocks = random_blocks(1024, 5120, seed=17)
+def test_auto_split_gemv_rounds_once_at_the_store(dtype, rows: int) -> None:
+    blocks = random_blocks(rows, 5120, seed=17)
     raw = torch.from_numpy(np.random.default_rng(17).normal(0.0, 1.0, size=(1, 5120)).astype(np.float32)).to(dtype)
     narrow = run_auto(blocks, raw.numpy() if dtype == torch.float16 else raw.float().numpy(), dtype=dtype)
     assert narrow.dtype == dtype
@@ -255,13 +260,14 @@ def test_auto_split_gemv_rounds_once_at_the_store(dtype) -> None:
     np.testing.assert_array_equal(narrow.float().cpu().numpy(), wide.to(dtype).float().cpu().numpy())
 
 
+@pytest.mark.parametrize("rows", (1024, 4000))
 @pytest.mark.parametrize("bad", (np.nan, np.inf, -np.inf))
 @pytest.mark.parametrize("position", (0, 2600, 5119))
-def test_auto_split_gemv_carries_non_finite_activations_to_every_row(bad: float, position: int) -> None:
-    blocks = random_blocks(1024, 5120, seed=31)
+def test_auto_split_gemv_carries_non_finite_activations_to_every_row(bad: float, position: int, rows: int) -> None:
+    blocks = random_blocks(rows, 5120, seed=31)
     x = np.zeros((1, 5120), dtype=np.float32)
     x[0, position] = bad
     got = run_auto(blocks, x).cpu().numpy()
-    want = O.oracle_matmul(blocks, x, rows=1024, columns=5120)
+    want = O.oracle_matmul(blocks, x, rows=rows, columns=5120)
     assert int(np.count_nonzero(np.isfinite(got))) == 0
     assert O.compare(got, want)["pattern_mismatches"] == 0
