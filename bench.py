@@ -56,6 +56,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-model-stream", action="store_true")
     p.add_argument("--no-small-batch", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--prefill-probe", action="store_true",
+                   help="run only the M=512 prefill GEMMs (gate/up, down), 2 warm-up + --steps eager launches "
+                        "each, for rocprofv3 --pmc MFMA-utilisation passes")
     p.add_argument("--traffic-probe", action="store_true",
                    help="only launch the dominant kernel eagerly over the cold ring, then a plain copy of "
                         "COPY_BYTES, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
@@ -211,6 +214,20 @@ def main() -> int:
         b.record(stream)
         torch.cuda.synchronize()
         return a.elapsed_time(b) / replays
+
+    if args.prefill_probe:
+        # Eager launches only (counter collection serialises dispatches).
+        for name, K, N in C3_SHAPES:
+            lay = PackedTensorLayout.for_tensor(N, K)
+            blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
+            xp = synthetic.device_activations(PREFILL_BATCHES[0], K, seed=synthetic.SEED_BASE + 3, sigma=0.5)
+            for _ in range(2 + args.steps):
+                tq1_gemm(blk, xp, layout=lay, config=GemmConfig())
+            torch.cuda.synchronize()
+            del blk, xp
+        print(json.dumps({"prefill_probe": [name for name, _, _ in C3_SHAPES], "M": PREFILL_BATCHES[0],
+                          "launches": 2 + args.steps}), flush=True)
+        return 0
 
     # ---- config 1: ring of distinct weight copies, cold ----------------------------
     step_bytes = sum(packed_bytes(K, N) for _, K, N in C1_SHAPES)
