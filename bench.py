@@ -59,6 +59,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--prefill-probe", action="store_true",
                    help="run only the M=512 prefill GEMMs (gate/up, down), 2 warm-up + --steps eager launches "
                         "each, for rocprofv3 --pmc MFMA-utilisation passes")
+    p.add_argument("--traffic-batch", type=int, default=1,
+                   help="activation rows of the --traffic-probe launches (the library's dispatch for that batch)")
     p.add_argument("--traffic-probe", action="store_true",
                    help="only launch the dominant kernel eagerly over the cold ring, then a plain copy of "
                         "COPY_BYTES, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
@@ -249,14 +251,16 @@ def main() -> int:
     if args.traffic_probe:
         # Eager launches only (counter collection serialises dispatches): the dominant
         # kernel over the cold ring, then a plain copy of known size for calibration.
+        xt = xs[0] if args.traffic_batch == 1 else synthetic.device_activations(
+            args.traffic_batch, C1_SHAPES[0][1], seed=synthetic.SEED_BASE + 1)
         for s in range(args.steps):
-            tq1_matmul(weights[s % ring][0], xs[0], layout=layouts[0], config=config)
+            tq1_linear(weights[s % ring][0], xt, layout=layouts[0])
         src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(args.steps):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"traffic_probe": C1_SHAPES[0][0], "launches": args.steps,
+        print(json.dumps({"traffic_probe": C1_SHAPES[0][0], "batch": args.traffic_batch, "launches": args.steps,
                           "bytes_per_launch": packed_bytes(C1_SHAPES[0][1], C1_SHAPES[0][2]),
                           "copy_bytes": COPY_BYTES}), flush=True)
         return 0
