@@ -190,6 +190,29 @@ def test_argument_errors_are_reported_without_a_launch() -> None:
     assert rc == _lib.TERNEL_TQ1_EINVAL and "indices are empty" in _lib.last_error()
 
 
+@pytest.mark.parametrize(("M", "rows", "columns", "message"), [
+    (1, 0, 5120, "dimensions must be positive"),
+    (1, 256, -128, "dimensions must be positive"),
+    (0, 256, 5120, "empty batch dimension"),
+    (1, 2**31, 5120, "too large for 32-bit"),
+    (2**31, 256, 5120, "too large for 32-bit"),
+    (1, 256, 128 * (2**31 // 7 + 1), "too large for 32-bit"),
+])
+def test_geometry_limits_are_refused_before_any_launch(M: int, rows: int, columns: int, message: str) -> None:
+    """Sizes past the kernels' 32-bit row, batch and word indices fail with EINVAL on the
+    host, for every compute entry point, before any device memory is touched."""
+    handle = _lib.lib()
+    x = ctypes.c_char_p(b"x" * 16)
+    calls = {
+        "matmul": lambda: handle.ternel_tq1_matmul(x, x, x, M, rows, columns, 0, 0, 0, None, 0, None),
+        "gemm": lambda: handle.ternel_tq1_gemm(x, x, x, M, rows, columns, 0, 0, 0, None, 0, None),
+        "linear": lambda: handle.ternel_tq1_linear(x, x, x, M, rows, columns, 0, None, 0, None),
+    }
+    for name, call in calls.items():
+        assert call() == _lib.TERNEL_TQ1_EINVAL, name
+        assert message in _lib.last_error(), (name, _lib.last_error())
+
+
 def test_split_k_refusal_message() -> None:
     handle = _lib.lib()
     x = ctypes.c_char_p(b"x" * 16)
