@@ -418,6 +418,7 @@ def main() -> int:
 C4_LAYER = (("qkv", 5120, 8192), ("o", 8192, 5120), ("gate_up", 5120, 34816), ("down", 17408, 5120))
 C4_LAYERS = 64
 C4_VOCAB = 151936
+PREFILL_TOKENS = 8192
 HEAD_ROWS = 248320  # Bonsai 27B vocabulary: the tied lm_head (src/ternel_mlx/layout.py:179-192 census)
 
 
@@ -451,7 +452,22 @@ def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_s
     total = C4_LAYERS * sum(packed_bytes(K, N) for _, K, N in C4_LAYER)
     gather = graph_of(lambda: [tq1_get_rows(table, token, layout=table_layout, dtype=torch.float16) for _ in range(100)])
     gather_us = time_graph(gather) / 100 * 1e3
-    del graph, gather, weights, table
+    # A prefill's gather: 8192 random ids, 1120 packed bytes read and 10240 fp16 bytes
+    # written per row, HBM-bound on the writes.
+    ids = torch.randint(0, C4_VOCAB, (PREFILL_TOKENS,), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(synthetic.SEED_BASE + 45))
+    prefill_bytes = PREFILL_TOKENS * (packed_bytes(5120, 1) + 5120 * 2)
+    # PackedEmbedding gathers from its canonical row-major copy (a token's 1120 bytes
+    # contiguous); the packed layout spreads a row over 280 separate 256-byte segments.
+    from ternel_amd.kernels import tq1_get_rows_canonical, unpack_weights
+    rows_major = unpack_weights(table, layout=table_layout)
+    prefill = graph_of(lambda: [tq1_get_rows_canonical(rows_major, ids, layout=table_layout, dtype=torch.float16)
+                                for _ in range(10)])
+    prefill_us = time_graph(prefill, 5) / 10 * 1e3
+    from_packed = graph_of(lambda: [tq1_get_rows(table, ids, layout=table_layout, dtype=torch.float16)
+                                    for _ in range(10)])
+    from_packed_us = time_graph(from_packed, 5) / 10 * 1e3
+    del graph, gather, prefill, from_packed, weights, table, rows_major
     return {
         "workload": "BASELINE configs[4]: 64 x (QKV 5120->8192, O 8192->5120, gate+up 5120->34816 with the "
                     "fused SwiGLU epilogue, down 17408->5120) M=1 GEMVs + 1 embedding row of 151936x5120, "
@@ -461,6 +477,11 @@ def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_s
         "GB/s": round(total / (ms * 1e-3) / 1e9, 1),
         "frac_of_hbm_peak": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "embedding_row_us_graph": round(gather_us, 3),
+        "embedding_prefill": {"tokens": PREFILL_TOKENS, "table": "canonical rows (PackedEmbedding)",
+                              "us": round(prefill_us, 2), "bytes": prefill_bytes,
+                              "GB/s": round(prefill_bytes / prefill_us / 1e3, 1),
+                              "frac_of_hbm_peak": round(prefill_bytes / prefill_us / 1e3 / HBM_PEAK_GBS, 4),
+                              "packed_table_us": round(from_packed_us, 2)},
     }
 
 

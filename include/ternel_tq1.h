@@ -172,6 +172,17 @@ int ternel_tq1_get_rows(const uint32_t *packed, int64_t rows, int64_t columns, c
                         int64_t n_ids, void *out, int dtype, void *stream);
 
 /*
+ * The same gather over canonical block rows (rows x columns/128 blocks of 28
+ * bytes, row-major, as the reference's sidecar stores them,
+ * src/bonsai_tq1/format.py:94-122), 4-byte aligned: a token's blocks are one
+ * contiguous run, where the packed layout spreads a row over a 256-byte
+ * segment per word. Serves tq1_get_rows, src/ternel_mlx/kernels.py:1360-1398,
+ * for tables that are only gathered from (an untied embedding).
+ */
+int ternel_tq1_get_rows_canonical(const uint8_t *blocks, int64_t rows, int64_t columns, const int64_t *ids,
+                                  int64_t n_ids, void *out, int dtype, void *stream);
+
+/*
  * packed_matmul dispatch (src/ternel_mlx/modules.py:425-457): the LUT23 path
  * or an MFMA form and its split, from (M, rows, columns, dtype). ws sized by
  * ternel_tq1_linear_workspace_bytes, same contract as ternel_tq1_matmul's.

@@ -39,6 +39,7 @@ SIGNATURES = {
     "ternel_tq1_gemm": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p, _size, _p]),
     "ternel_tq1_gemm_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
     "ternel_tq1_get_rows": (_int, [_p, _i64, _i64, _p, _i64, _p, _int, _p]),
+    "ternel_tq1_get_rows_canonical": (_int, [_p, _i64, _i64, _p, _i64, _p, _int, _p]),
     "ternel_tq1_linear_kernel": (_int, [_i64, _i64, _i64, _int]),
     "ternel_tq1_swiglu": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _p, _size, _p]),
     "ternel_tq1_swiglu_workspace_bytes": (_size, [_i64, _i64, _i64, _int]),

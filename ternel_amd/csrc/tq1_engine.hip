@@ -291,38 +291,89 @@ __global__ __launch_bounds__(kThreads) void deinterleave_kernel(const uint32_t *
 }
 
 // ---------------------------------------------------------------------------
-// get_rows_kernel: one thread per (token, group, code slot) writes the 5 (or
-// 3) weights that byte holds: (t - 1) * scale, evaluated in fp32 and rounded
-// to T (exact for fp16 and fp32). Ids outside [0, rows) give zeros
-// (src/ternel_mlx/kernels.py:869-880).
+// get_rows_kernel: one thread per (token, group, run of 8 weights) writes its
+// run with one 16-byte store (two for fp32): each value (t - 1) * scale,
+// evaluated in fp32 and rounded to T (exact for fp16 and fp32). Weight w of a
+// block is digit w % 5 of code byte w / 5 -- the tail byte is code byte 25,
+// its digits 0-2 weights 125-127 -- so a run reads the scale word and the two
+// words that hold its two or three code bytes, and takes its digits from a
+// table of each byte's five base-3 digits (2 bits each) in LDS. Ids outside
+// [0, rows) give zeros (src/ternel_mlx/kernels.py:869-880). CANON: the table
+// is canonical block rows (row r, group g at byte (r * G + g) * 28), so a
+// token's 1,120 bytes are one contiguous run; else the packed layout, where a
+// row's words lie in separate 256-byte segments.
 // ---------------------------------------------------------------------------
-template <typename T>
+constexpr int kGatherRuns = kBlockWeights / 8;  // 8-weight runs per block
+
+template <typename T, bool CANON>
 __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__restrict__ packed,
                                                             int64_t rows, int G,
                                                             const int64_t *__restrict__ ids,
-                                                            int64_t n_ids, T *__restrict__ out) {
-    const int per_token = G * kCodeSlots;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= per_token) return;
-    const int g = i / kCodeSlots;
-    const int s = i - g * kCodeSlots;
-    const int first = s < kFullSlots ? 5 * s : 125;
-    const int count = s < kFullSlots ? 5 : 3;
-    const int byte_index = 2 + s;
-    for (int64_t t = blockIdx.y; t < n_ids; t += gridDim.y) {
-        const int64_t id = ids[t];
-        T *o = out + t * static_cast<int64_t>(G) * kBlockWeights + g * kBlockWeights + first;
-        if (id < 0 || id >= rows) {
-            for (int d = 0; d < count; ++d) o[d] = from_f32<T>(0.0f);
-            continue;
-        }
-        const float scale = half_bits_to_float(packed[packed_word_index(id, G, g, 0)]);
-        uint32_t b = (packed[packed_word_index(id, G, g, byte_index >> 2)] >> ((byte_index & 3) * 8)) & 0xffu;
-        for (int d = 0; d < count; ++d) {
+                                                            int64_t n_ids, T *__restrict__ out,
+                                                            int vector_out) {
+    __shared__ uint32_t digits[256];  // byte b -> its digits, digit i in bits 2i..2i+1
+    {
+        uint32_t b = threadIdx.x, d = 0;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
             const uint32_t q = b / 3u;
-            const uint32_t trit = b - 3u * q;
+            d |= (b - 3u * q) << (2 * i);
             b = q;
-            o[d] = from_f32<T>((static_cast<float>(trit) - 1.0f) * scale);
+        }
+        digits[threadIdx.x] = d;
+    }
+    __syncthreads();
+    const int64_t per_token = static_cast<int64_t>(G) * kGatherRuns;
+    const int64_t total = n_ids * per_token;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * kThreads) {
+        const int64_t t = i / per_token;
+        const int rem = static_cast<int>(i - t * per_token);
+        const int g = rem / kGatherRuns;
+        const int k = rem - g * kGatherRuns;
+        const int64_t id = ids[t];
+        float v[8];
+        if (id < 0 || id >= rows) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+        } else {
+            const int w0 = 8 * k;
+            const int b0 = w0 / 5;       // first code byte of the run
+            const int phase = w0 - 5 * b0;  // its first digit
+            const int byte0 = 2 + b0;    // byte offset in the 28-byte block
+            const int word = byte0 >> 2;
+            auto word_at = [&](int j) {
+                return CANON ? packed[(id * G + g) * kBlockWords + j] : packed[packed_word_index(id, G, g, j)];
+            };
+            const float scale = half_bits_to_float(word_at(0));
+            const uint32_t lo = word_at(word);
+            // A run never needs a byte past the block: k = 14, 15 use two bytes.
+            const uint32_t hi = word + 1 < kBlockWords ? word_at(word + 1) : 0u;
+            const uint64_t window = ((static_cast<uint64_t>(hi) << 32) | lo) >> ((byte0 & 3) * 8);
+            const uint32_t d = digits[window & 0xffu] | (digits[(window >> 8) & 0xffu] << 10) |
+                               (digits[(window >> 16) & 0xffu] << 20);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t trit = (d >> (2 * (phase + e))) & 3u;
+                v[e] = (static_cast<float>(trit) - 1.0f) * scale;
+            }
+        }
+        T *o = out + t * static_cast<int64_t>(G) * kBlockWeights + g * kBlockWeights + 8 * k;
+        if (vector_out) {
+            if constexpr (sizeof(T) == 4) {
+                reinterpret_cast<float4 *>(o)[0] = float4{v[0], v[1], v[2], v[3]};
+                reinterpret_cast<float4 *>(o)[1] = float4{v[4], v[5], v[6], v[7]};
+            } else {
+                uint32_t pk[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    pk[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e]))) |
+                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e + 1]))) << 16);
+                *reinterpret_cast<uint4 *>(o) = uint4{pk[0], pk[1], pk[2], pk[3]};
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = from_f32<T>(v[e]);
         }
     }
 }
@@ -2289,6 +2340,45 @@ int check_packed_pointer(const void *packed) {
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
+template <bool CANON>
+int launch_get_rows(const uint32_t *table, int64_t rows, int64_t columns, const int64_t *ids, int64_t n_ids,
+                    void *out, int dtype, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(1, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
+    if (n_ids <= 0) return fail(TERNEL_TQ1_EINVAL, "indices are empty");
+    if ((rc = check_packed_pointer(table)) != TERNEL_TQ1_OK) return rc;
+    if (!ids || !out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    const int G = static_cast<int>(columns / kBlockWeights);
+    if (n_ids > INT64_MAX / (static_cast<int64_t>(G) * kGatherRuns))
+        return fail(TERNEL_TQ1_EINVAL, "too many indices for one gather");
+    // Grid-stride over (token, group, run): at most 8 workgroups of 256 per CU
+    // (an uncapped grid measured the same on MI355X: 8192 tokens 27.1 us
+    // against 25.4).
+    const int64_t threads = n_ids * G * kGatherRuns;
+    const int64_t cap = static_cast<int64_t>(device_cu_count()) * 8;
+    const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(threads, kThreads), cap)));
+    const int vector_out = reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case TERNEL_TQ1_F16:
+            hipLaunchKernelGGL((get_rows_kernel<_Float16, CANON>), grid, dim3(kThreads), 0, s, table, rows, G, ids,
+                               n_ids, static_cast<_Float16 *>(out), vector_out);
+            break;
+        case TERNEL_TQ1_BF16:
+            hipLaunchKernelGGL((get_rows_kernel<bf16_t, CANON>), grid, dim3(kThreads), 0, s, table, rows, G, ids,
+                               n_ids, static_cast<bf16_t *>(out), vector_out);
+            break;
+        default:
+            hipLaunchKernelGGL((get_rows_kernel<float, CANON>), grid, dim3(kThreads), 0, s, table, rows, G, ids,
+                               n_ids, static_cast<float *>(out), vector_out);
+            break;
+    }
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
 extern "C" {
 
 const char *ternel_tq1_last_error(void) { return g_last_error; }
@@ -2491,34 +2581,15 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
 
 int ternel_tq1_get_rows(const uint32_t *packed, int64_t rows, int64_t columns, const int64_t *ids, int64_t n_ids,
                         void *out, int dtype, void *stream) {
-    g_last_error[0] = '\0';
-    int rc;
-    if ((rc = check_geometry(1, rows, columns)) != TERNEL_TQ1_OK) return rc;
-    if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
-    if (n_ids <= 0) return fail(TERNEL_TQ1_EINVAL, "indices are empty");
-    if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
-    if (!ids || !out) return fail(TERNEL_TQ1_EINVAL, "null pointer");
-    const int G = static_cast<int>(columns / kBlockWeights);
-    const int per_token = G * kCodeSlots;
-    const dim3 grid(static_cast<unsigned>(ceil_div(per_token, kThreads)),
-                    static_cast<unsigned>(n_ids < 65535 ? n_ids : 65535));
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    switch (dtype) {
-        case TERNEL_TQ1_F16:
-            hipLaunchKernelGGL((get_rows_kernel<_Float16>), grid, dim3(kThreads), 0, s, packed, rows, G, ids, n_ids,
-                               static_cast<_Float16 *>(out));
-            break;
-        case TERNEL_TQ1_BF16:
-            hipLaunchKernelGGL((get_rows_kernel<bf16_t>), grid, dim3(kThreads), 0, s, packed, rows, G, ids, n_ids,
-                               static_cast<bf16_t *>(out));
-            break;
-        default:
-            hipLaunchKernelGGL((get_rows_kernel<float>), grid, dim3(kThreads), 0, s, packed, rows, G, ids, n_ids,
-                               static_cast<float *>(out));
-            break;
-    }
-    TQ1_LAUNCH_CHECK();
-    return TERNEL_TQ1_OK;
+    return launch_get_rows<false>(packed, rows, columns, ids, n_ids, out, dtype, stream);
+}
+
+int ternel_tq1_get_rows_canonical(const uint8_t *blocks, int64_t rows, int64_t columns, const int64_t *ids,
+                                  int64_t n_ids, void *out, int dtype, void *stream) {
+    if (reinterpret_cast<uintptr_t>(blocks) % 4)
+        return fail(TERNEL_TQ1_EINVAL, "canonical blocks must be 4-byte aligned");
+    return launch_get_rows<true>(reinterpret_cast<const uint32_t *>(blocks), rows, columns, ids, n_ids, out, dtype,
+                                 stream);
 }
 
 size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {

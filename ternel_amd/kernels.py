@@ -268,13 +268,7 @@ def tq1_swiglu(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLay
     return out
 
 
-def tq1_get_rows(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
-                 dtype: torch.dtype) -> torch.Tensor:
-    """Decode the rows named by ``indices`` (1-D); reference tq1_get_rows, kernels.py:1360-1398.
-
-    Ids outside ``[0, rows)`` read as zeros, as the reference kernel does.
-    """
-    check_packed(packed, layout=layout)
+def _gather_ids(indices: torch.Tensor, dtype: torch.dtype, device) -> torch.Tensor:
     if dtype not in ACTIVATION_DTYPES:
         raise FormatError(f"output dtype must be one of {ACTIVATION_DTYPES}, got {dtype}")
     if indices.ndim != 1:
@@ -283,11 +277,38 @@ def tq1_get_rows(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedT
         raise FormatError("indices are empty")
     if indices.dtype not in (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8):
         raise FormatError(f"indices must be an integer tensor, got {indices.dtype}")
-    ids = indices.to(device=packed.device, dtype=torch.int64).contiguous()
+    return indices.to(device=device, dtype=torch.int64).contiguous()
+
+
+def tq1_get_rows(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
+                 dtype: torch.dtype) -> torch.Tensor:
+    """Decode the rows named by ``indices`` (1-D); reference tq1_get_rows, kernels.py:1360-1398.
+
+    Ids outside ``[0, rows)`` read as zeros, as the reference kernel does.
+    """
+    check_packed(packed, layout=layout)
+    ids = _gather_ids(indices, dtype, packed.device)
     out = torch.empty((ids.numel(), layout.columns), dtype=dtype, device=packed.device)
     _lib.check(_lib.lib().ternel_tq1_get_rows(
         packed.data_ptr(), layout.rows, layout.columns, ids.data_ptr(), ids.numel(), out.data_ptr(),
         _DTYPE_CODE[dtype], _stream(packed.device)))
+    return out
+
+
+def tq1_get_rows_canonical(blocks: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
+                           dtype: torch.dtype) -> torch.Tensor:
+    """``tq1_get_rows`` over canonical ``(rows, G, 28)`` uint8 device blocks (``unpack_weights``):
+    a token's blocks are one contiguous run, so a gather reads only the rows it returns."""
+    if blocks.dtype != torch.uint8 or tuple(blocks.shape) != tuple(layout.canonical_shape):
+        raise FormatError(f"canonical blocks must be uint8 {tuple(layout.canonical_shape)}, "
+                          f"got {blocks.dtype} {tuple(blocks.shape)}")
+    if blocks.device.type != "cuda" or not blocks.is_contiguous():
+        raise FormatError("canonical blocks must be a contiguous device tensor")
+    ids = _gather_ids(indices, dtype, blocks.device)
+    out = torch.empty((ids.numel(), layout.columns), dtype=dtype, device=blocks.device)
+    _lib.check(_lib.lib().ternel_tq1_get_rows_canonical(
+        blocks.data_ptr(), layout.rows, layout.columns, ids.data_ptr(), ids.numel(), out.data_ptr(),
+        _DTYPE_CODE[dtype], _stream(blocks.device)))
     return out
 
 
@@ -300,6 +321,7 @@ __all__ = [
     "packed_shape",
     "tq1_gemm",
     "tq1_get_rows",
+    "tq1_get_rows_canonical",
     "tq1_linear",
     "tq1_matmul",
     "unpack_weights",

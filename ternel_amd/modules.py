@@ -29,6 +29,7 @@ from .kernels import (
     packed_shape,
     tq1_gemm,
     tq1_get_rows,
+    tq1_get_rows_canonical,
     tq1_matmul,
     tq1_swiglu,
     unpack_weights,
@@ -228,10 +229,25 @@ class PackedEmbedding(_PackedWeight):
         return f"{self.layout.rows} x {self.layout.columns}, tile={self.layout.tile}, {self.dtype}"
 
     def forward(self, indices: torch.Tensor) -> torch.Tensor:
-        """Rows for ``indices`` of any shape; ids outside the table read as zeros."""
+        """Rows for ``indices`` of any shape; ids outside the table read as zeros.
+
+        Gathers read a canonical row-major copy of the table (``row_blocks``): in the
+        packed layout a row's words lie in separate 256-byte segments, so a gather
+        would fetch whole segments for 4 bytes each."""
         flat = indices.reshape(-1)
-        rows = tq1_get_rows(self.packed, flat, layout=self.layout, dtype=self.dtype)
+        rows = tq1_get_rows_canonical(self.row_blocks(), flat, layout=self.layout, dtype=self.dtype)
         return rows.reshape(*indices.shape, self.layout.columns)
+
+    def row_blocks(self) -> torch.Tensor:
+        """The table as canonical ``(rows, G, 28)`` device blocks, derived from the packed
+        words on first use and again whenever they are replaced or written (28 bytes per
+        128 weights: 170 MB for a 151,936 x 5120 table). Not part of the state dict. Call it
+        once before capturing a graph that gathers, so the capture holds no rebuild."""
+        key = (self.packed.data_ptr(), self.packed._version, self.packed.device)
+        if getattr(self, "_row_blocks_key", None) != key:
+            self._row_blocks = unpack_weights(self.packed, layout=self.layout)
+            self._row_blocks_key = key
+        return self._row_blocks
 
     def as_linear(self, x: torch.Tensor) -> torch.Tensor:
         """Tied output head: the embedding table used as a matmul."""

@@ -11,7 +11,8 @@ from torch import nn
 from oracle import tq1_oracle as O
 from tests.gpu_util import layout, pack, random_blocks, to_dev
 from ternel_amd.format import FormatError
-from ternel_amd.kernels import tq1_get_rows
+from ternel_amd import _lib
+from ternel_amd.kernels import tq1_get_rows, tq1_get_rows_canonical
 from ternel_amd.layout import pack_blocks
 from ternel_amd.modules import PackedEmbedding, PackedLinear, packed_matmul, replace_with_packed, select_kernel
 
@@ -46,6 +47,56 @@ def test_get_rows_repeats_and_out_of_range_ids() -> None:
     np.testing.assert_array_equal(got[0], got[4])
     assert not got[5:].any()
     assert got[2].any() and got[3].any()
+
+
+@pytest.mark.parametrize(("rows", "columns"), ((1024, 5120), (300, 256), (64, 128)))
+@pytest.mark.parametrize("dtype", (torch.float32, torch.float16, torch.bfloat16))
+def test_canonical_gather_is_bit_identical_to_the_packed_one(rows: int, columns: int, dtype) -> None:
+    """Both table layouts give the same bits, including repeats, both ends of every block
+    (runs 14 and 15 read the last word) and ids outside the table (zeros)."""
+    blocks = random_blocks(rows, columns, seed=rows + columns)
+    rng = np.random.default_rng(rows)
+    ids = torch.tensor(np.concatenate([[0, rows - 1, 3, 3, rows, -5], rng.integers(0, rows, size=61)]),
+                       dtype=torch.int64, device="cuda")
+    lay = layout(rows, columns)
+    canonical = torch.from_numpy(blocks).cuda()
+    got = tq1_get_rows_canonical(canonical, ids, layout=lay, dtype=dtype)
+    packed = tq1_get_rows(pack(blocks), ids, layout=lay, dtype=dtype)
+    assert torch.equal(got.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       packed.view(torch.int16 if dtype != torch.float32 else torch.int32))
+    assert not got[4:6].any()
+    if dtype != torch.bfloat16:
+        host_ids = ids[:4].cpu().numpy()
+        want = O.get_rows_reference(blocks, host_ids, rows=rows, columns=columns,
+                                    dtype=np.float32 if dtype == torch.float32 else np.float16)
+        np.testing.assert_array_equal(got[:4].cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("entry", ("packed", "canonical"))
+def test_gather_into_an_unaligned_output(entry: str) -> None:
+    """An output that is not 16-byte aligned takes element stores, with the same values."""
+    rows, columns = 300, 256
+    blocks = random_blocks(rows, columns, seed=77)
+    lay = layout(rows, columns)
+    table = pack(blocks) if entry == "packed" else torch.from_numpy(blocks).cuda()
+    ids = torch.tensor([5, 299, 0, 150], dtype=torch.int64, device="cuda")
+    aligned = (tq1_get_rows if entry == "packed" else tq1_get_rows_canonical)(table, ids, layout=lay,
+                                                                              dtype=torch.float16)
+    buf = torch.zeros(ids.numel() * columns + 1, dtype=torch.float16, device="cuda")
+    fn = _lib.lib().ternel_tq1_get_rows if entry == "packed" else _lib.lib().ternel_tq1_get_rows_canonical
+    _lib.check(fn(table.data_ptr(), rows, columns, ids.data_ptr(), ids.numel(), buf[1:].data_ptr(),
+                  _lib.DTYPE_F16, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert buf[0].item() == 0
+    assert torch.equal(buf[1:].view(ids.numel(), columns).view(torch.int16), aligned.view(torch.int16))
+
+
+def test_canonical_gather_rejects_a_wrong_table() -> None:
+    lay = layout(256, 256)
+    ids = torch.zeros(1, dtype=torch.int64, device="cuda")
+    with pytest.raises(FormatError, match="canonical blocks"):
+        tq1_get_rows_canonical(torch.zeros((256, 2, 27), dtype=torch.uint8, device="cuda"), ids, layout=lay,
+                               dtype=torch.float32)
 
 
 def test_get_rows_rejects_bad_indices() -> None:
@@ -130,6 +181,18 @@ def test_tied_head_is_the_same_arithmetic_as_a_linear() -> None:
     linear.load_blocks(blocks)
     x = torch.randn(4, columns, device="cuda", dtype=torch.float16)
     np.testing.assert_array_equal(embedding.as_linear(x).cpu().numpy(), linear(x).cpu().numpy())
+
+
+def test_packed_embedding_gathers_from_reloaded_weights() -> None:
+    """The row-major copy the gathers read follows the packed words when they are reloaded."""
+    rows, columns = 256, 256
+    module = PackedEmbedding(layout(rows, columns), dtype=torch.float32)
+    tokens = torch.tensor([0, 17, 255], device="cuda")
+    for seed in (1, 2):
+        blocks = random_blocks(rows, columns, seed=seed)
+        module.load_blocks(blocks)
+        want = O.get_rows_reference(blocks, tokens.cpu().numpy(), rows=rows, columns=columns)
+        np.testing.assert_array_equal(module(tokens).cpu().numpy(), want)
 
 
 def test_out_of_range_token_reads_zero() -> None:

@@ -188,6 +188,10 @@ def test_argument_errors_are_reported_without_a_launch() -> None:
     assert rc == _lib.TERNEL_TQ1_EINVAL and "at most 64 activation rows" in _lib.last_error()
     rc = handle.ternel_tq1_get_rows(None, 256, 5120, None, 0, None, 0, None)
     assert rc == _lib.TERNEL_TQ1_EINVAL and "indices are empty" in _lib.last_error()
+    rc = handle.ternel_tq1_get_rows_canonical(ctypes.c_void_p(4098), 256, 5120, None, 1, None, 0, None)
+    assert rc == _lib.TERNEL_TQ1_EINVAL and "4-byte aligned" in _lib.last_error()
+    rc = handle.ternel_tq1_get_rows_canonical(ctypes.c_void_p(4096), 256, 5120, None, 0, None, 0, None)
+    assert rc == _lib.TERNEL_TQ1_EINVAL and "indices are empty" in _lib.last_error()
 
 
 @pytest.mark.parametrize(("M", "rows", "columns", "message"), [
