@@ -56,6 +56,13 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-model-stream", action="store_true")
     p.add_argument("--no-small-batch", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--stream-ceiling", action="store_true",
+                   help="measure the single-launch HBM read ceiling (libternel_probe.so) at the configs' matrix "
+                        "sizes and print one JSON line")
+    p.add_argument("--phase-profile", action="store_true",
+                   help="load the phase-timestamp build of the engine and summarise where a cold M=1 GEMV "
+                        "launch spends its time, per configs[1] matrix (one JSON line each), next to the "
+                        "graph-timed stream GEMV and LUT23 kernel")
     p.add_argument("--prefill-probe", action="store_true",
                    help="run only the M=512 prefill GEMMs (gate/up, down), 2 warm-up + --steps eager launches "
                         "each, for rocprofv3 --pmc MFMA-utilisation passes")
@@ -175,6 +182,10 @@ def main() -> int:
     args = parse()
     if args.trace_summary:
         return trace_summary(args.trace_summary)
+    if args.phase_profile:
+        # before anything imports the package: the ctypes binding loads this build
+        os.environ.setdefault("TERNEL_TQ1_LIBRARY", os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                                 "ternel_amd", "_lib", "libternel_tq1_profile.so"))
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the TQ1 path runs on a single MI355X in this build "
@@ -184,8 +195,8 @@ def main() -> int:
     import torch
 
     from ternel_amd import synthetic
-    from ternel_amd.kernels import (GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_get_rows, tq1_linear,
-                                    tq1_matmul, tq1_swiglu)
+    from ternel_amd.kernels import (GemmConfig, MatmulConfig, pack_weights, tq1_gemm_words, tq1_get_rows_words, tq1_linear_words,
+                                    tq1_matmul_words, tq1_swiglu_words)
     from ternel_amd.layout import PackedTensorLayout
     from ternel_amd.modules import select_kernel
 
@@ -217,6 +228,12 @@ def main() -> int:
         torch.cuda.synchronize()
         return a.elapsed_time(b) / replays
 
+    if args.stream_ceiling:
+        return stream_ceiling(torch, dev, graph_of, time_graph)
+    if args.phase_profile:
+        return phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedTensorLayout,
+                             MatmulConfig, graph_of, time_graph)
+
     if args.prefill_probe:
         # Eager launches only (counter collection serialises dispatches).
         for name, K, N in C3_SHAPES:
@@ -224,7 +241,7 @@ def main() -> int:
             blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
             xp = synthetic.device_activations(PREFILL_BATCHES[0], K, seed=synthetic.SEED_BASE + 3, sigma=0.5)
             for _ in range(2 + args.steps):
-                tq1_gemm(blk, xp, layout=lay, config=GemmConfig())
+                tq1_gemm_words(blk, xp, layout=lay, config=GemmConfig())
             torch.cuda.synchronize()
             del blk, xp
         print(json.dumps({"prefill_probe": [name for name, _, _ in C3_SHAPES], "M": PREFILL_BATCHES[0],
@@ -242,7 +259,7 @@ def main() -> int:
 
     def step(r: int) -> None:
         for i, lay in enumerate(layouts):
-            tq1_matmul(weights[r][i], xs[i], layout=lay, config=config)
+            tq1_matmul_words(weights[r][i], xs[i], layout=lay, config=config)
 
     for w in range(args.warmup):
         step(w % ring)
@@ -254,7 +271,7 @@ def main() -> int:
         xt = xs[0] if args.traffic_batch == 1 else synthetic.device_activations(
             args.traffic_batch, C1_SHAPES[0][1], seed=synthetic.SEED_BASE + 1)
         for s in range(args.steps):
-            tq1_linear(weights[s % ring][0], xt, layout=layouts[0])
+            tq1_linear_words(weights[s % ring][0], xt, layout=layouts[0])
         src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(args.steps):
@@ -277,7 +294,7 @@ def main() -> int:
     dominant = 0
     dom_name, dom_K, dom_N = C1_SHAPES[dominant]
     dom_bytes = packed_bytes(dom_K, dom_N)
-    dom_graph = graph_of(lambda: [tq1_matmul(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant],
+    dom_graph = graph_of(lambda: [tq1_matmul_words(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant],
                                              config=config) for s in range(args.steps)])
     graph_launch_ms = time_graph(dom_graph) / args.steps
     del dom_graph
@@ -287,7 +304,7 @@ def main() -> int:
     pairs = [events() for _ in range(args.steps)]
     for s in range(args.steps):
         pairs[s][0].record(stream)
-        tq1_matmul(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant], config=config)
+        tq1_matmul_words(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant], config=config)
         pairs[s][1].record(stream)
     torch.cuda.synchronize()
     launch_ms = sorted(a.elapsed_time(b) for a, b in pairs)
@@ -295,12 +312,12 @@ def main() -> int:
     median_launch_ms = launch_ms[len(launch_ms) // 2]
     per_matrix = {}
     for i, (name, K, N) in enumerate(C1_SHAPES):
-        g = graph_of(lambda i=i: [tq1_matmul(weights[s % ring][i], xs[i], layout=layouts[i], config=config)
+        g = graph_of(lambda i=i: [tq1_matmul_words(weights[s % ring][i], xs[i], layout=layouts[i], config=config)
                                   for s in range(ring * 4)])
         ms = time_graph(g) / (ring * 4)
         per_matrix[name] = {"graph_ms_per_launch": round(ms, 5), "GB/s": round(packed_bytes(K, N) / (ms * 1e-3) / 1e9, 1)}
         del g
-    warm = graph_of(lambda: [tq1_matmul(weights[0][dominant], xs[dominant], layout=layouts[dominant], config=config)
+    warm = graph_of(lambda: [tq1_matmul_words(weights[0][dominant], xs[dominant], layout=layouts[dominant], config=config)
                              for _ in range(100)])
     warm_ms = time_graph(warm) / 100
     del warm
@@ -312,7 +329,7 @@ def main() -> int:
             xm = [synthetic.device_activations(M, K, seed=synthetic.SEED_BASE + 2 + M) for _, K, _ in C1_SHAPES]
             row = {}
             for i, (name, K, N) in enumerate(C1_SHAPES):
-                g = graph_of(lambda i=i: [tq1_linear(weights[s % ring][i], xm[i], layout=layouts[i])
+                g = graph_of(lambda i=i: [tq1_linear_words(weights[s % ring][i], xm[i], layout=layouts[i])
                                           for s in range(ring * 2)])
                 ms = time_graph(g) / (ring * 2)
                 del g
@@ -379,7 +396,7 @@ def main() -> int:
                 blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
                 xp = synthetic.device_activations(M, K, seed=synthetic.SEED_BASE + 3, sigma=0.5)
                 reps = max(4, 20 * 512 // M)
-                g = graph_of(lambda: [tq1_gemm(blk, xp, layout=lay, config=GemmConfig()) for _ in range(reps)])
+                g = graph_of(lambda: [tq1_gemm_words(blk, xp, layout=lay, config=GemmConfig()) for _ in range(reps)])
                 ms = time_graph(g) / reps
                 tflops = 2 * M * K * N / (ms * 1e-3) / 1e12
                 prefill[name] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2),
@@ -393,7 +410,7 @@ def main() -> int:
         heads = [pack_weights(synthetic.device_blocks(HEAD_ROWS, 5120, seed=synthetic.SEED_BASE + 50 + i),
                               layout=head_layout) for i in range(2)]  # 2 x 278 MB: every launch reads HBM
         xh = synthetic.device_activations(1, 5120, seed=synthetic.SEED_BASE + 51)
-        g = graph_of(lambda: [tq1_matmul(heads[s % 2], xh, layout=head_layout, config=MatmulConfig())
+        g = graph_of(lambda: [tq1_matmul_words(heads[s % 2], xh, layout=head_layout, config=MatmulConfig())
                               for s in range(20)])
         ms = time_graph(g) / 20
         head_bytes = packed_bytes(5120, HEAD_ROWS)
@@ -405,13 +422,148 @@ def main() -> int:
 
     # ---- config 4: 64-layer weight stream + one embedding row -------------------
     if not args.no_model_stream:
-        result["model_stream"] = model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_swiglu,
+        result["model_stream"] = model_stream(torch, synthetic, pack_weights, tq1_matmul_words, tq1_get_rows_words, tq1_swiglu_words,
                                               PackedTensorLayout, MatmulConfig, graph_of, time_graph)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
 
     print(json.dumps(result), flush=True)
+    return 0
+
+
+PHASES = ("start", "own tables written", "tables ready (barrier)", "blocks summed", "partial stored and acknowledged",
+          "arrival counted", "fix-up done")
+
+
+def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedTensorLayout, MatmulConfig,
+                  graph_of, time_graph) -> int:
+    """Per configs[1] matrix: three cold launches of the M=1 GEMV (the LUT23
+    kernel) with the phase stamps of every wave (100 MHz wall clock, lane 0):
+    each phase's time after the launch's first wave started, and -- free of
+    any clock offset between XCDs -- each phase's duration per wave; beside
+    them the graph-timed GEMV of the same build over the cold ring."""
+    import ctypes
+    import statistics
+
+    from ternel_amd import _lib
+
+    handle = _lib.lib()
+    fn = handle.ternel_tq1_profile_stamps
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    max_waves = 8192
+    buf = (ctypes.c_ulonglong * (max_waves * len(PHASES) + max_waves * 2))()
+    ring = 14
+    for i, (name, K, N) in enumerate(C1_SHAPES):
+        lay = PackedTensorLayout.for_tensor(N, K)
+        weights = [pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
+                   for r in range(ring)]
+        x = synthetic.device_activations(1, K, seed=synthetic.SEED_BASE + 1 + i)
+        graph_ms = time_graph(graph_of(lambda: [tq1_matmul_words(weights[r % ring], x, layout=lay)
+                                                for r in range(ring * 4)])) / (ring * 4)
+        rows = []
+        for r in range(3):  # three cold launches, each over a copy last read 13 launches ago
+            fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
+            tq1_matmul_words(weights[(r + 5) % ring], x, layout=lay)
+            waves = fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
+            stamps = [[buf[w * 8 + p] for p in range(len(PHASES))] for w in range(waves)]
+            stamps = [st for st in stamps if st[0]]
+            t0 = min(st[0] for st in stamps)
+            last_stamps, t0_last = stamps, t0
+            rows.append({PHASES[p]: [(st[p] - t0) * 10 / 1000 for st in stamps if st[p]] for p in range(len(PHASES))})
+        summary = {}
+        for p, phase in enumerate(PHASES):
+            values = [v for row in rows for v in row[phase]]
+            if values:
+                values.sort()
+                summary[phase] = {"min_us": round(values[0], 2),
+                                  "median_us": round(statistics.median(values), 2),
+                                  "p95_us": round(values[int(0.95 * (len(values) - 1))], 2),
+                                  "max_us": round(values[-1], 2)}
+        # Offset-free figures (a wave's own stamps): each phase's duration per
+        # wave, and how far apart the waves of one workgroup started.
+        durations = {}
+        for p in range(1, len(PHASES)):
+            d = sorted((st[p] - st[p - 1]) / 100 for st in last_stamps if st[p] and st[p - 1])
+            if d:
+                durations[f"{PHASES[p - 1]} -> {PHASES[p]}"] = {
+                    "median_us": round(statistics.median(d), 2), "p95_us": round(d[int(0.95 * (len(d) - 1))], 2)}
+        spreads = sorted((max(st[0] for st in last_stamps[g:g + 8]) - min(st[0] for st in last_stamps[g:g + 8])) / 100
+                         for g in range(0, len(last_stamps) - 7, 8))
+        print(json.dumps({"phase_profile": name, "K": K, "N": N, "waves": len(rows[0]["start"]),
+                          "gemv_graph_us": round(graph_ms * 1e3, 3),
+                          "phases_after_first_wave_start": summary,
+                          "phase_durations_per_wave": durations,
+                          "workgroup_start_spread_us (8-wave groups)": {"median": round(statistics.median(spreads), 2),
+                                                                        "max": round(spreads[-1], 2)},
+                          "clock": "s_memrealtime (100 MHz), lane 0 of every wave, 3 cold launches"}), flush=True)
+        del weights
+    return 0
+
+
+STREAM_SIZES = (("qkv", 9_175_040), ("gate_up", 19_496_960), ("layer", 76_840_960), ("long", 320 * 2**20))
+# (load width in bytes, loads per lane, threads per workgroup)
+STREAM_SHAPES = ((4, 7, 512), (4, 28, 256), (16, 2, 512), (16, 4, 512), (16, 8, 256), (16, 16, 256))
+STREAM_POOL_BYTES = 1536 * 2**20  # rotation pool: every launch reads bytes no cache holds
+
+
+def stream_ceiling(torch, dev, graph_of, time_graph) -> int:
+    """Single-launch read ceiling: for each matrix size and load shape, 64 launches replayed
+    from one graph, each over a different region of a 1.5 GiB pool (cold), of a kernel that
+    only loads (every load issued before the first use) and writes one word per wave."""
+    import ctypes
+
+    from ternel_amd.build import PROBE_PATH
+
+    if not PROBE_PATH.exists():
+        raise RuntimeError(f"{PROBE_PATH} is missing; build with `python -m ternel_amd.build`")
+    probe = ctypes.CDLL(str(PROBE_PATH))
+    probe.ternel_probe_chunk_bytes.restype = ctypes.c_int64
+    probe.ternel_probe_chunk_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
+    probe.ternel_probe_stream.restype = ctypes.c_int
+    probe.ternel_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    probe.ternel_probe_last_error.restype = ctypes.c_char_p
+    pool = torch.ones(STREAM_POOL_BYTES // 4, dtype=torch.int32, device=dev)
+    max_waves = max(size // probe.ternel_probe_chunk_bytes(w, l) for _, size in STREAM_SIZES
+                    for w, l, _ in STREAM_SHAPES)
+    out = torch.zeros(max_waves, dtype=torch.int32, device=dev)
+    launches = 64
+    rows = []
+    for name, size in STREAM_SIZES:
+        for width, loads, threads in STREAM_SHAPES:
+            chunk = probe.ternel_probe_chunk_bytes(width, loads)
+            waves = size // chunk
+            nbytes = waves * chunk
+            stride = -(-nbytes // 4096) * 4096
+            regions = min(launches, STREAM_POOL_BYTES // stride)
+
+            def launch(r, waves=waves, width=width, loads=loads, threads=threads, stride=stride, regions=regions):
+                offset = (r % regions) * stride
+                rc = probe.ternel_probe_stream(pool.data_ptr() + offset, STREAM_POOL_BYTES - offset, out.data_ptr(),
+                                               out.numel(), waves, width, loads, threads,
+                                               torch.cuda.current_stream(dev).cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(probe.ternel_probe_last_error().decode())
+
+            g = graph_of(lambda: [launch(r) for r in range(launches)])
+            ms = min(time_graph(g) for _ in range(3)) / launches
+            del g
+            rows.append({"size": name, "bytes": nbytes, "width": width, "loads_per_lane": loads,
+                         "threads": threads, "workgroups": -(-waves // (threads // 64)), "regions": regions,
+                         "us": round(ms * 1e3, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+            print(json.dumps(rows[-1]), flush=True)
+    best = {}
+    for row in rows:
+        if row["size"] not in best or row["GB/s"] > best[row["size"]]["GB/s"]:
+            best[row["size"]] = row
+    print(json.dumps({"stream_ceiling": {k: {"us": v["us"], "GB/s": v["GB/s"],
+                                            "frac_of_hbm_peak": round(v["GB/s"] / HBM_PEAK_GBS, 4),
+                                            "shape": [v["width"], v["loads_per_lane"], v["threads"]]}
+                                        for k, v in best.items()},
+                      "timing": f"{launches} launches per graph over distinct pool regions, best of 3 replays"}),
+          flush=True)
     return 0
 
 
@@ -422,7 +574,7 @@ PREFILL_TOKENS = 8192
 HEAD_ROWS = 248320  # Bonsai 27B vocabulary: the tied lm_head (src/ternel_mlx/layout.py:179-192 census)
 
 
-def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_swiglu, PackedTensorLayout,
+def model_stream(torch, synthetic, pack_weights, tq1_matmul_words, tq1_get_rows_words, tq1_swiglu_words, PackedTensorLayout,
                  MatmulConfig, graph_of, time_graph) -> dict:
     """64 sequential layers of M=1 GEMVs (4.92 GB of packed weights,
     larger than every cache, so each token reads them cold), then one embedding row. The
@@ -441,16 +593,16 @@ def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_s
         for layer in range(C4_LAYERS):
             for i, (name, K, _) in enumerate(C4_LAYER):
                 if name == "gate_up":
-                    tq1_swiglu(weights[layer][i], xs[K], layout=layouts[i])
+                    tq1_swiglu_words(weights[layer][i], xs[K], layout=layouts[i])
                 else:
-                    tq1_matmul(weights[layer][i], xs[K], layout=layouts[i], config=config)
-        tq1_get_rows(table, token, layout=table_layout, dtype=torch.float16)
+                    tq1_matmul_words(weights[layer][i], xs[K], layout=layouts[i], config=config)
+        tq1_get_rows_words(table, token, layout=table_layout, dtype=torch.float16)
 
     graph = graph_of(token_pass)
     replays = 5
     ms = time_graph(graph, replays)
     total = C4_LAYERS * sum(packed_bytes(K, N) for _, K, N in C4_LAYER)
-    gather = graph_of(lambda: [tq1_get_rows(table, token, layout=table_layout, dtype=torch.float16) for _ in range(100)])
+    gather = graph_of(lambda: [tq1_get_rows_words(table, token, layout=table_layout, dtype=torch.float16) for _ in range(100)])
     gather_us = time_graph(gather) / 100 * 1e3
     # A prefill's gather: 8192 random ids, 1120 packed bytes read and 10240 fp16 bytes
     # written per row, HBM-bound on the writes.
@@ -464,7 +616,7 @@ def model_stream(torch, synthetic, pack_weights, tq1_matmul, tq1_get_rows, tq1_s
     prefill = graph_of(lambda: [tq1_get_rows_canonical(rows_major, ids, layout=table_layout, dtype=torch.float16)
                                 for _ in range(10)])
     prefill_us = time_graph(prefill, 5) / 10 * 1e3
-    from_packed = graph_of(lambda: [tq1_get_rows(table, ids, layout=table_layout, dtype=torch.float16)
+    from_packed = graph_of(lambda: [tq1_get_rows_words(table, ids, layout=table_layout, dtype=torch.float16)
                                     for _ in range(10)])
     from_packed_us = time_graph(from_packed, 5) / 10 * 1e3
     del graph, gather, prefill, from_packed, weights, table, rows_major

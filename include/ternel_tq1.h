@@ -34,12 +34,18 @@
  * both of `dtype` (TERNEL_TQ1_F16 is the graded type; BF16/F32 also accepted by
  * the LUT path), fp32 accumulation throughout.
  *
- * Workspaces: ternel_tq1_matmul's workspace starts with a fixed 64 KiB region
- * of split-K arrival counters that must be zero the first time the workspace
- * is used; every call leaves it zero again, so one zero-filled workspace can
+ * Workspaces: a split workspace starts with a fixed 64 KiB region of
+ * arrival counters whose last 32-bit word is the workspace's error word, then
+ * a fixed 32 MiB region of the LUT23 kernel's published pieces (64-bit
+ * {value, flag} slots), then the fp32 partials of the other split kernels. The
+ * first two regions must be zero the first time the workspace is used; every
+ * successful call leaves them zero again, so one zero-filled workspace can
  * serve calls of any shape (the reference's stream-K contract,
  * cuda/tq1_lut23_streamk.cu:320-334). Calls sharing one workspace must not
- * overlap in time.
+ * overlap in time (one workspace per stream). A kernel whose bounded wait for
+ * another workgroup's published partial gives up sets the error word
+ * (ternel_tq1_workspace_error) and may leave counters or slots set: zero the
+ * workspace again before reusing it.
  */
 #ifndef TERNEL_TQ1_H
 #define TERNEL_TQ1_H
@@ -115,6 +121,25 @@ int ternel_tq1_deinterleave(const uint32_t *packed, int64_t rows, int64_t column
                             void *stream);
 
 /*
+ * The reference's tiled pair -> packed words, on the device, with the
+ * fail-closed scan folded in: codes is uint8 [rows/tile][G][26][tile], scales
+ * uint16 (raw fp16 bits) [rows/tile][G][tile] (src/ternel_mlx/layout.py:100-108),
+ * tile divides rows; packed receives ternel_tq1_packed_words(rows, columns)
+ * words. counters (two uint64, overwritten) receive the code bytes above 242 in
+ * slots 0..24 and above 26 in slot 25, as validate_packed_codes counts them
+ * (src/ternel_mlx/packing.py:29-48); the caller rejects the weight when either
+ * is nonzero. Replaces unpack_blocks + the upload of
+ * src/ternel_mlx/packing.py:67-83.
+ */
+int ternel_tq1_words_from_tiled(const uint8_t *codes, const uint16_t *scales, int64_t rows, int64_t columns,
+                                int64_t tile, uint32_t *packed, uint64_t *counters, void *stream);
+
+/* Packed words -> the tiled pair (the exact inverse); replaces pack_blocks,
+ * src/ternel_mlx/packing.py:51-65, for a module's codes/scales state. */
+int ternel_tq1_tiled_from_words(const uint32_t *packed, int64_t rows, int64_t columns, int64_t tile, uint8_t *codes,
+                                uint16_t *scales, void *stream);
+
+/*
  * LUT23 product y = x @ W^T for small M (decode GEMV at M=1, small batches).
  * Replaces tq1_matmul, src/ternel_mlx/kernels.py:1215-1271 (and the CUDA
  * launchers launch_tq1_g128_gemv_v1, cuda/tq1_g128_gemv.cu:169-180, and
@@ -123,6 +148,8 @@ int ternel_tq1_deinterleave(const uint32_t *packed, int64_t rows, int64_t column
  * A split is reduced inside the same launch, in chunk order (deterministic).
  * ws: at least ternel_tq1_matmul_workspace_bytes(...) bytes (0 when the split
  * resolves to 1; ws may then be NULL); see the workspace contract above.
+ * A split batch whose (row block, batch tile) counters or pieces exceed their
+ * regions runs as several launches of as many rows as they hold, in order.
  */
 int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
                       int64_t columns, int dtype, int batch_tile, int k_split, void *ws, size_t ws_bytes,
@@ -218,6 +245,25 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
 int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M, int64_t rows, int64_t columns,
                       int dtype, void *ws, size_t ws_bytes, void *stream);
 size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype);
+
+/*
+ * Reads a workspace's error word (synchronises `stream`): *error = 0, or a
+ * bitmask of the kernels whose bounded wait for a published partial gave up
+ * (1 = the LUT23 kernel's split-K fix-up, 2 = the wide GEMM's stream-K
+ * reduction). No
+ * counterpart in the reference, whose fix-ups (cuda/tq1_lut23_streamk.cu:
+ * 194-256) spin without a bound; here a wait that cannot complete is reported
+ * instead of hanging the device or summing unpublished data.
+ */
+int ternel_tq1_workspace_error(const void *ws, size_t ws_bytes, int *error, void *stream);
+
+/*
+ * Sets how many times such a wait polls before giving up (default 2^22, about
+ * 0.2 s); a negative limit makes every wait give up at once, which is how the
+ * tests drive the error path from the host. Returns the previous limit. Takes
+ * effect for launches issued after the call. No counterpart in the reference.
+ */
+int ternel_tq1_set_spin_limit(int limit);
 
 #ifdef __cplusplus
 }

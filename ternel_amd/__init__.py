@@ -19,8 +19,9 @@ from .format import (
     validate_blocks,
     validate_packed_codes,
 )
-from .kernels import GemmConfig, MatmulConfig, tq1_gemm, tq1_get_rows, tq1_linear, tq1_matmul
+from .kernels import (GemmConfig, MatmulConfig, tq1_gemm, tq1_gemm_words, tq1_get_rows, tq1_get_rows_words,
+                      tq1_linear_words, tq1_matmul, tq1_matmul_words)
 from .layout import PackedTensorLayout, pack_blocks, select_tile, unpack_blocks
 from .modules import PackedEmbedding, PackedLinear, packed_matmul, replace_with_packed
 
-__version__ = "0.1.0"
+__version__ = "0.3.0"

@@ -9,7 +9,16 @@ from __future__ import annotations
 import ctypes
 from pathlib import Path
 
+import os
+
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libternel_tq1.so"
+
+
+def library_path() -> Path:
+    """The engine library, or the build of the same C ABI that
+    ``TERNEL_TQ1_LIBRARY`` names when the library is first loaded (the
+    phase-profile variant, for bench.py --phase-profile)."""
+    return Path(os.environ.get("TERNEL_TQ1_LIBRARY") or LIB_PATH)
 
 TERNEL_TQ1_OK = 0
 TERNEL_TQ1_EINVAL = -1
@@ -34,6 +43,8 @@ SIGNATURES = {
     "ternel_tq1_from_q2": (_int, [_p, _i64, _p, _p, _p]),
     "ternel_tq1_interleave": (_int, [_p, _i64, _i64, _p, _p]),
     "ternel_tq1_deinterleave": (_int, [_p, _i64, _i64, _p, _p]),
+    "ternel_tq1_words_from_tiled": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
+    "ternel_tq1_tiled_from_words": (_int, [_p, _i64, _i64, _i64, _p, _p, _p]),
     "ternel_tq1_matmul": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p, _size, _p]),
     "ternel_tq1_matmul_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
     "ternel_tq1_gemm": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p, _size, _p]),
@@ -45,6 +56,8 @@ SIGNATURES = {
     "ternel_tq1_swiglu_workspace_bytes": (_size, [_i64, _i64, _i64, _int]),
     "ternel_tq1_linear": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _p, _size, _p]),
     "ternel_tq1_linear_workspace_bytes": (_size, [_i64, _i64, _i64, _int]),
+    "ternel_tq1_workspace_error": (_int, [_p, _size, _p, _p]),
+    "ternel_tq1_set_spin_limit": (_int, [_int]),
 }
 
 
@@ -62,12 +75,13 @@ _LIB: ctypes.CDLL | None = None
 def lib() -> ctypes.CDLL:
     global _LIB
     if _LIB is None:
-        if not LIB_PATH.exists():
+        path = library_path()
+        if not path.exists():
             raise NativeLibraryMissing(
-                f"{LIB_PATH} is missing; build it with `python -m ternel_amd.build` "
+                f"{path} is missing; build it with `python -m ternel_amd.build` "
                 "(the TQ1 engine has no CPU fallback)"
             )
-        handle = ctypes.CDLL(str(LIB_PATH))
+        handle = ctypes.CDLL(str(path))
         for name, (restype, argtypes) in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = restype

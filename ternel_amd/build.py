@@ -18,6 +18,11 @@ SOURCE = PACKAGE_DIR / "csrc" / "tq1_engine.hip"
 INCLUDE_DIR = REPO_ROOT / "include"
 LIB_DIR = PACKAGE_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libternel_tq1.so"
+# measurement-only streaming probe (bench.py --stream-ceiling); not part of the C ABI
+PROBE_SOURCE = PACKAGE_DIR / "csrc" / "stream_probe.hip"
+PROBE_PATH = LIB_DIR / "libternel_probe.so"
+# the same engine source with phase timestamps in the M=1 GEMV (bench.py --phase-profile)
+PROFILE_PATH = LIB_DIR / "libternel_tq1_profile.so"
 ARCH = "gfx950"
 
 # Packed fp32 instructions are disabled for every HIP translation unit: some of
@@ -47,18 +52,34 @@ def hipcc() -> str:
     return found
 
 
+def _command(source: Path, target: Path, extra: list[str]) -> list[str]:
+    return [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE_DIR}", str(source), "-o", str(target.with_suffix(".so.tmp"))]
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile the library (always recompiles) and return its path."""
+    """Compile the engine library, its phase-profile variant and the streaming
+    probe, in parallel (always recompiles); return the engine library's path."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", str(SOURCE), "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    env = dict(os.environ)
-    result = subprocess.run(cmd, capture_output=True, text=True, env=env)
-    if result.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({result.returncode}):\n{result.stdout}\n{result.stderr}")
-    os.replace(tmp, LIB_PATH)
+    jobs = [(SOURCE, LIB_PATH, []), (PROBE_SOURCE, PROBE_PATH, []),
+            (SOURCE, PROFILE_PATH, ["-DTERNEL_TQ1_PROFILE"])]
+    running = []
+    for source, target, extra in jobs:
+        cmd = _command(source, target, extra)
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        running.append((target, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                                                  env=dict(os.environ))))
+    failures = []
+    for target, proc in running:
+        out, err = proc.communicate()
+        if proc.returncode != 0:
+            failures.append(f"{target.name}: hipcc failed ({proc.returncode}):\n{out}\n{err}")
+    if failures:
+        for target, _ in running:
+            target.with_suffix(".so.tmp").unlink(missing_ok=True)
+        raise RuntimeError("\n".join(failures))
+    for target, _ in running:
+        os.replace(target.with_suffix(".so.tmp"), target)
     return LIB_PATH
 
 

@@ -26,9 +26,14 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
+#include <set>
+#include <utility>
 #include <type_traits>
 
 #include "ternel_tq1.h"
@@ -57,6 +62,31 @@ constexpr int kLutFloats = kTailBase + 27;                    // 927
 constexpr int kTasksPerGroup = 2 * kFullSlots + 1;            // L2 x25, L3 x25, tail
 
 constexpr int kThreads = 256;
+
+// Split workspaces start with 64 KiB of 32-bit counters; the last one is the
+// error word (the host section keeps every kernel's counters below it).
+constexpr int kWorkspaceCounterBytes = 64 * 1024;
+constexpr int kWorkspaceErrorSlot = kWorkspaceCounterBytes / 4 - 1;
+
+// Phase timestamps (built only with -DTERNEL_TQ1_PROFILE, into a separate
+// library that bench.py --phase-profile loads): lane 0 of each wave of the
+// M = 1 stream GEMV writes the 100 MHz wall clock at its phase boundaries.
+constexpr int kPhaseWaves = 8192;
+constexpr int kPhaseSlots = 8;
+#ifdef TERNEL_TQ1_PROFILE
+__device__ unsigned long long g_phase_stamps[kPhaseWaves][kPhaseSlots];
+#define TQ1_PHASE(wave_id, slot)                                                                     \
+    do {                                                                                             \
+        __builtin_amdgcn_sched_barrier(0);                                                           \
+        if ((threadIdx.x & 63) == 0 && (wave_id) < kPhaseWaves)                                      \
+            g_phase_stamps[(wave_id)][(slot)] = static_cast<unsigned long long>(wall_clock64());      \
+        __builtin_amdgcn_sched_barrier(0);                                                           \
+    } while (0)
+#else
+#define TQ1_PHASE(wave_id, slot) \
+    do {                         \
+    } while (0)
+#endif
 
 thread_local char g_last_error[512] = "";
 
@@ -276,6 +306,82 @@ __global__ __launch_bounds__(kThreads) void interleave_kernel(const uint32_t *__
     const int64_t g = tg % G;
     const int64_t row = (tg / G) * kTileRows + lane;
     packed[w] = row < rows ? canonical[(row * G + g) * kBlockWords + j] : 0u;
+}
+
+// ---------------------------------------------------------------------------
+// The reference's tiled pair <-> packed words (an exact byte permutation,
+// src/ternel_mlx/packing.py:51-83 composed with the packed-word interleave):
+// codes[r / tile][g][s][r % tile] is block byte 2 + s of block (r, g),
+// scales[r / tile][g][r % tile] its bytes 0-1. One thread per packed word.
+// The upload also counts illegal code bytes exactly as validate_packed_codes
+// (src/ternel_mlx/packing.py:29-48) does: slots 0..24 above 242, slot 25
+// above 26.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void words_from_tiled_kernel(const uint8_t *__restrict__ codes,
+                                                                    const uint16_t *__restrict__ scales,
+                                                                    uint32_t *__restrict__ packed, int64_t rows,
+                                                                    int64_t G, int64_t tile, int64_t total_words,
+                                                                    unsigned long long *counters) {
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    uint32_t bad_regular = 0, bad_tail = 0;
+    if (w < total_words) {
+        const int lane = static_cast<int>(w % kTileRows);
+        const int64_t rest = w / kTileRows;
+        const int j = static_cast<int>(rest % kBlockWords);
+        const int64_t tg = rest / kBlockWords;
+        const int64_t g = tg % G;
+        const int64_t row = (tg / G) * kTileRows + lane;
+        uint32_t word = 0;
+        if (row < rows) {
+            const int64_t tt = row / tile, rr = row % tile;
+            const uint8_t *code = codes + ((tt * G + g) * kCodeSlots) * tile + rr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int byte = 4 * j + i;
+                uint32_t v;
+                if (byte < 2) {
+                    v = (scales[(tt * G + g) * tile + rr] >> (8 * byte)) & 0xffu;
+                } else {
+                    const int slot = byte - 2;
+                    v = code[slot * tile];
+                    if (slot < kFullSlots) bad_regular += v > 242u;
+                    else bad_tail += v > kMaxTailByte;
+                }
+                word |= v << (8 * i);
+            }
+        }
+        packed[w] = word;
+    }
+    bad_regular = wave_sum_u32(bad_regular);
+    bad_tail = wave_sum_u32(bad_tail);
+    if ((threadIdx.x & 63) == 0) {
+        if (bad_regular) atomicAdd(&counters[0], static_cast<unsigned long long>(bad_regular));
+        if (bad_tail) atomicAdd(&counters[1], static_cast<unsigned long long>(bad_tail));
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void tiled_from_words_kernel(const uint32_t *__restrict__ packed,
+                                                                    uint8_t *__restrict__ codes,
+                                                                    uint16_t *__restrict__ scales, int64_t rows,
+                                                                    int64_t G, int64_t tile, int64_t total_words) {
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (w >= total_words) return;
+    const int lane = static_cast<int>(w % kTileRows);
+    const int64_t rest = w / kTileRows;
+    const int j = static_cast<int>(rest % kBlockWords);
+    const int64_t tg = rest / kBlockWords;
+    const int64_t g = tg % G;
+    const int64_t row = (tg / G) * kTileRows + lane;
+    if (row >= rows) return;
+    const uint32_t word = packed[w];
+    const int64_t tt = row / tile, rr = row % tile;
+    if (j == 0) scales[(tt * G + g) * tile + rr] = static_cast<uint16_t>(word & 0xffffu);
+    uint8_t *code = codes + ((tt * G + g) * kCodeSlots) * tile + rr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int byte = 4 * j + i;
+        if (byte >= 2) code[(byte - 2) * tile] = static_cast<uint8_t>(word >> (8 * i));
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void deinterleave_kernel(const uint32_t *__restrict__ packed,
@@ -536,27 +642,38 @@ __device__ __forceinline__ void split_word(uint32_t word, uint32_t base, uint32_
     split_pair(__builtin_amdgcn_perm(0u, word, 0x0c030c01u), base, lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
 }
 
-// Adds partial[0..k) (stride apart) left to right. The agent-coherent loads of
-// up to 32 chunks are all issued before the first add, so a split costs one
-// memory round trip here rather than one per chunk.
-__device__ __forceinline__ float sum_partials_in_order(const float *src, int64_t stride, int k) {
+// Adds the k published pieces of one output (stride apart) left to right.
+// Each is a 64-bit slot {fp32 value, flag 1}, written by one atomic store: the
+// count of arrivals says every piece has been stored, the flag that its store
+// is visible here. All loads of a batch of up to 32 are in flight at once (one
+// memory round trip per batch); a slot whose flag is not visible yet is polled
+// (at most spin_limit times -- a negative limit gives up at once, the tests'
+// way in), and every slot is cleared for the next call.
+__device__ __forceinline__ float sum_pieces_in_order(uint64_t *src, int64_t stride, int k, int spin_limit,
+                                                     bool &failed) {
     constexpr int kBatch = 32;
+    if (spin_limit < 0) failed = true;
     float a = 0.0f;
     for (int z0 = 0; z0 < k; z0 += kBatch) {
-        float v[kBatch];
+        uint64_t v[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
             v[u] = z0 + u < k ? __hip_atomic_load(src + (z0 + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : 0.0f;
-        if (z0 == 0) {
-            a = v[0];
+                              : 0;
 #pragma unroll
-            for (int u = 1; u < kBatch; ++u)
-                if (u < k) a += v[u];
-        } else {
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                if (z0 + u < k) a += v[u];
+        for (int u = 0; u < kBatch; ++u) {
+            if (z0 + u >= k) continue;
+            for (int spin = 0; (v[u] >> 32) == 0 && !failed; ++spin) {
+                if (spin >= spin_limit) {
+                    failed = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                v[u] = __hip_atomic_load(src + (z0 + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            const float f = __uint_as_float(static_cast<uint32_t>(v[u]));
+            a = z0 + u == 0 ? f : a + f;
+            __hip_atomic_store(src + (z0 + u) * stride, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     return a;
@@ -577,8 +694,8 @@ __device__ __forceinline__ T swiglu_pair(T gate, T up) {
 template <typename T, int C, int BT, bool GLU = false, int KW = 1>
 __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     const uint32_t *__restrict__ packed, const T *__restrict__ x, T *__restrict__ y,
-    float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
-    int k_split) {
+    uint64_t *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
+    int k_split, int spin_limit) {
     // KW waves share each 64-row tile: wave stream s sums blocks
     // [s * CB, (s + 1) * CB) of every sub-chunk, so all of a sub-chunk's words
     // can be in flight from the start without one wave stalling on their issue.
@@ -609,6 +726,10 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     // branching around their loads.
     const int load_tile = min(tile, (N + kTileRows - 1) / kTileRows - 1);
     const uint32_t *row_words = packed + static_cast<int64_t>(load_tile) * G * kTileGroupWords + lane;
+    const int lut_wave_id =
+        ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * KW * (kThreads / 64) + (tid >> 6);
+    (void)lut_wave_id;
+    TQ1_PHASE(lut_wave_id, 0);  // wave start
 
     float acc[BT];
 #pragma unroll
@@ -649,7 +770,9 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         // previous sub-chunk's table and exchange reads before this.)
         if (KW == 1 && g0 != g_begin) __syncthreads();
         build_lut_tables<T, C, BT, NT>(lut, xv, tid);
+        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 1);  // own table entries written
         __syncthreads();
+        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 2);  // tables ready
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
             if (c + kLutLoadAhead < CB) {
@@ -714,6 +837,7 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         run(xv, g0);
     }
 
+    TQ1_PHASE(lut_wave_id, 3);  // all blocks summed
     // 4. Output. With GLU, rows 2r and 2r+1 are the gate and up rows of one
     // SwiGLU unit and sit in adjacent lanes: each lane rounds its value as the
     // unfused linear would, the even lane takes its partner's and writes
@@ -734,37 +858,46 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         for (int j = 0; j < BT; ++j) store(j, acc[j]);
         return;
     }
-    // Split: publish the partial with agent-coherent stores (they bypass the
-    // per-XCD L2, so no cache writeback is needed), wait until they are
-    // acknowledged, then count this chunk in. The workgroup that brings the
-    // count to k_split adds the chunks in chunk order with agent-coherent loads.
+    // Split: publish the partial as {value, flag} with one 64-bit agent-scope
+    // store per output, then count this chunk in. The workgroup that brings
+    // the count to k_split adds the chunks in chunk order, waiting on each
+    // slot's flag -- which is what makes the hand-off correct with relaxed
+    // atomics only (no cache writeback or invalidate). Waiting for the stores
+    // to be acknowledged before counting is for speed alone: the last arriver
+    // then finds every flag on its first load (without it, measured on MI355X,
+    // its fix-up took a second round trip: gate/up 9.5 -> 10.7 us).
     if (row_ok) {
 #pragma unroll
         for (int j = 0; j < BT; ++j)
             if (b0 + j < M)
-                __hip_atomic_store(partial + (static_cast<int64_t>(blockIdx.z) * M + b0 + j) * N + row, acc[j],
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(partial + (static_cast<int64_t>(blockIdx.z) * M + b0 + j) * N + row,
+                                   (uint64_t{1} << 32) | __float_as_uint(acc[j]), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
     wait_vector_memory();
+    TQ1_PHASE(lut_wave_id, 4);  // partial stored and acknowledged
     __syncthreads();
     unsigned *counter = counters + static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
     if (tid == 0)
         s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  static_cast<unsigned>(k_split - 1);
     __syncthreads();
+    TQ1_PHASE(lut_wave_id, 5);  // arrival counted
     if (!s_last) return;
     const int64_t stride = static_cast<int64_t>(M) * N;
+    bool failed = false;
 #pragma unroll
     for (int j = 0; j < BT; ++j) {
-        const float *src = partial + static_cast<int64_t>(b0 + j) * N + row;
-        store(j, row_ok && b0 + j < M ? sum_partials_in_order(src, stride, k_split) : 0.0f);
+        uint64_t *src = partial + static_cast<int64_t>(b0 + j) * N + row;
+        store(j, row_ok && b0 + j < M ? sum_pieces_in_order(src, stride, k_split, spin_limit, failed) : 0.0f);
     }
+    if (__builtin_amdgcn_ballot_w64(failed) && lane == 0)
+        __hip_atomic_fetch_or(counters + kWorkspaceErrorSlot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();  // every wave has read its slots before the counter is re-armed
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    TQ1_PHASE(lut_wave_id, 6);  // fix-up done
 }
 
-// The elementwise SwiGLU step over a linear's output whose rows alternate
-// gate, up: z[i] = SiLU(y[2i]) * y[2i+1] (N even, so pairs never straddle a
-// batch row).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const T *__restrict__ y, T *__restrict__ z,
                                                                 int64_t pairs) {
@@ -1317,7 +1450,7 @@ constexpr size_t wide_lds_bytes(int nb) {
 }
 constexpr int wide_frag_floats(int nb) { return nb * 16 * 64; }
 constexpr int kBufferRsrcFlags = 0x00020000;               // gfx9 raw buffer: 32-bit data format
-constexpr int kWideTileSlots = 8192;                       // stream-K counter pairs (arrivals, publications)
+constexpr int kWideTileSlots = 8184;                       // stream-K counter pairs (arrivals, publications)
 
 __device__ __forceinline__ int direct_target_unit(int u) { return u < 15 ? u : (u < 30 ? u + 1 : (u == 30 ? 15 : 31)); }
 
@@ -1328,7 +1461,9 @@ struct WideGeometry {
     int tiles;       // tiles_n * ceil(M / (32 NB))
     int units;       // tiles * G
     int vector_rows; // y rows start 16-byte aligned (y aligned, N % 8 == 0)
+    int spin_limit;  // polls of the publication count before the last arriver gives up
 };
+
 
 // Units are counted in 32 bits: at most 16384 tiles x 32768 groups.
 __device__ __forceinline__ int wide_unit_begin(int units, int p, int P) {
@@ -1400,6 +1535,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     // 64-row block b at byte b * 1792 + j * 256 + r * 4 (the packed layout).
     extern __shared__ __attribute__((aligned(16))) unsigned char wide_lds[];
     __shared__ unsigned s_last;
+    __shared__ unsigned s_published;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1706,15 +1842,25 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             return;
         }
         // Last to arrive: wait (bounded) until the others' partials are published.
+        // A wait that gives up sets the workspace error word and leaves both
+        // counters as they are -- a late publication must not carry into the
+        // next call; the host re-zeroes the workspace after reading the error.
         if (tid == 0) {
-            for (int spin = 0; spin < (1 << 22); ++spin) {
+            bool published = false;
+            for (int spin = 0; spin <= geo.spin_limit; ++spin) {
                 if (__hip_atomic_load(counters + kWideTileSlots + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
-                    static_cast<unsigned>(q1 - q0))
+                    static_cast<unsigned>(q1 - q0)) {
+                    published = true;
                     break;
+                }
                 __builtin_amdgcn_s_sleep(2);
             }
+            s_published = published;
+            if (!published)
+                __hip_atomic_fetch_or(counters + kWorkspaceErrorSlot, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
+        const bool published = s_published;
         // The sum runs in workgroup order q0..q1: the partials of q0..p-1, this
         // workgroup's accumulators, then the partials of p+1..q1. It is formed
         // in place in acc -- (prefix) + acc equals acc + (prefix) exactly in
@@ -1772,7 +1918,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                 store_frag(t, nb0 + i, out);
             }
         }
-        if (tid == 0) {
+        if (tid == 0 && published) {
             __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(counters + kWideTileSlots + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1865,6 +2011,27 @@ int64_t packed_words(int64_t rows, int64_t columns) {
     return ceil_div(rows, kTileRows) * (columns / kBlockWeights) * kTileGroupWords;
 }
 
+// Dynamic LDS above 64 KiB needs hipFuncSetAttribute once per kernel and
+// device; the set of (kernel, device) pairs already opted in is shared by all
+// threads.
+int ensure_lds_attribute(const void *kernel, int bytes) {
+    static std::mutex mu;
+    static std::set<std::pair<const void *, int>> done;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({kernel, dev})) return TERNEL_TQ1_OK;
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done.insert({kernel, dev});
+    return TERNEL_TQ1_OK;
+}
+
+// Polls of one published value before a kernel's bounded wait gives up and
+// sets the workspace error word (a negative limit makes every such wait give
+// up at once: the tests' way to drive the error path from the host).
+std::atomic<int> g_spin_limit{1 << 22};
+
 int check_dtype(int dtype) {
     if (dtype != TERNEL_TQ1_F16 && dtype != TERNEL_TQ1_BF16 && dtype != TERNEL_TQ1_F32)
         return fail(TERNEL_TQ1_EINVAL, "unsupported dtype code %d", dtype);
@@ -1894,6 +2061,19 @@ constexpr int64_t kLutMaxChunks = 20;
 // always written past it.
 constexpr int kCounterSlots = 16384;
 constexpr size_t kCounterRegionBytes = kCounterSlots * sizeof(unsigned);
+static_assert(kCounterRegionBytes == kWorkspaceCounterBytes, "one counter region");
+// The last counter slot is the workspace's error word: a kernel whose bounded
+// wait gave up sets it (ternel_tq1_workspace_error reads it). Counters of every
+// kernel stay below it.
+constexpr int kErrorSlot = kCounterSlots - 1;
+static_assert(kErrorSlot == kWorkspaceErrorSlot, "one error word");
+constexpr int kUsableCounters = kCounterSlots - 16;
+// The LUT23 kernel's published pieces follow the counters in a region of
+// their own: each 64-bit slot holds a flag that must be zero between calls, so
+// no other kernel's partials may ever land there.
+constexpr size_t kLutRegionBytes = 32u << 20;
+// Partials of every other split kernel start here.
+constexpr size_t kPartialOffset = kCounterRegionBytes + kLutRegionBytes;
 
 struct LutPlan {
     int batch_tile;
@@ -1902,7 +2082,8 @@ struct LutPlan {
     int chunk_groups;  // groups per workgroup, a multiple of chunk
     int k_split;
     int64_t row_blocks;
-    int64_t batch_tiles;
+    int64_t batch_tiles;        // of one launch
+    int64_t launch_vectors;     // activation rows per launch (a batch above it runs in several)
     size_t counter_bytes;
     size_t partial_bytes;
 };
@@ -1973,18 +2154,49 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
         (plan->chunk >= 8 || plan->row_blocks * plan->batch_tiles * plan->k_split <= 3 * device_cu_count()))
         plan->waves = 2;
     if (plan->k_split > 65535) return fail(TERNEL_TQ1_EINVAL, "K too large for one launch");
-    if (plan->k_split > 1 && plan->row_blocks * plan->batch_tiles > kCounterSlots)
-        return fail(TERNEL_TQ1_EINVAL, "%lld row blocks x %lld batch tiles exceed the %d split-K counters",
-                    static_cast<long long>(plan->row_blocks), static_cast<long long>(plan->batch_tiles),
-                    kCounterSlots);
+    // A split launch needs one arrival counter per (row block, batch tile):
+    // a batch past what the counter region holds runs as several launches
+    // (in order on the stream, each leaving its counters zero for the next).
+    plan->launch_vectors = M;
+    if (plan->k_split > 1 && plan->row_blocks * plan->batch_tiles > kUsableCounters) {
+        const int64_t tiles = kUsableCounters / plan->row_blocks;
+        if (tiles < 1)
+            return fail(TERNEL_TQ1_EINVAL, "%lld row blocks exceed the %d split-K counters",
+                        static_cast<long long>(plan->row_blocks), kUsableCounters);
+        plan->launch_vectors = tiles * plan->batch_tile;
+        plan->batch_tiles = tiles;
+    }
+    if (plan->batch_tiles > 65535) {
+        plan->batch_tiles = 65535;
+        plan->launch_vectors = std::min<int64_t>(plan->launch_vectors, 65535 * static_cast<int64_t>(plan->batch_tile));
+    }
+    if (plan->k_split > 1) {
+        // The pieces of one launch must fit the LUT region: fewer vectors per
+        // launch, or -- when not even one batch tile fits -- no split.
+        const int64_t per_vector = static_cast<int64_t>(plan->k_split) * rows * sizeof(uint64_t);
+        int64_t fit = static_cast<int64_t>(kLutRegionBytes) / per_vector;
+        fit -= fit % plan->batch_tile;
+        if (fit < plan->batch_tile) {
+            if (k_split > 1)
+                return fail(TERNEL_TQ1_EINVAL, "k split %d of %lld rows needs more split-K workspace than the %zu-byte "
+                            "region holds", k_split, static_cast<long long>(rows), kLutRegionBytes);
+            plan->k_split = 1;
+            plan->chunk_groups = static_cast<int>(G);
+            while (plan->chunk_groups % plan->chunk) plan->chunk /= 2;
+        } else if (plan->launch_vectors > fit) {
+            plan->launch_vectors = fit;
+            plan->batch_tiles = fit / plan->batch_tile;
+        }
+    }
     plan->counter_bytes = plan->k_split > 1 ? kCounterRegionBytes : 0;
-    plan->partial_bytes =
-        plan->k_split > 1 ? static_cast<size_t>(plan->k_split) * static_cast<size_t>(M) * rows * sizeof(float) : 0;
+    plan->partial_bytes = plan->k_split > 1 ? static_cast<size_t>(plan->k_split) *
+                                                  static_cast<size_t>(plan->launch_vectors) * rows * sizeof(uint64_t)
+                                            : 0;
     return TERNEL_TQ1_OK;
 }
 
 template <typename T, int C, int BT, bool GLU = false>
-void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *x, void *y, float *partial,
+void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *x, void *y, uint64_t *partial,
                        unsigned *counters, int64_t M, int64_t rows, int G, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.batch_tiles),
                     static_cast<unsigned>(plan.k_split));
@@ -1992,22 +2204,44 @@ void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *
         if (plan.waves == 2) {
             hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU, 2>), grid, dim3(2 * kThreads), 0, stream, packed,
                                static_cast<const T *>(x), static_cast<T *>(y), partial, counters,
-                               static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
+                               static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split,
+                               g_spin_limit.load());
             return;
         }
     }
     hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU>), grid, dim3(kThreads), 0, stream, packed,
                        static_cast<const T *>(x), static_cast<T *>(y), partial, counters, static_cast<int>(M),
-                       static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
+                       static_cast<int>(rows), G, plan.chunk_groups, plan.k_split, g_spin_limit.load());
 }
 
 template <typename T>
+int launch_lut_once(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+                    const LutPlan &plan, void *ws, hipStream_t stream, bool glu);
+
+// Runs the batch as ceil(M / launch_vectors) launches of at most
+// launch_vectors activation rows each.
+template <typename T>
 int launch_lut(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
                const LutPlan &plan, void *ws, hipStream_t stream, bool glu = false) {
+    const int64_t out_width = glu ? rows / 2 : rows;
+    for (int64_t m0 = 0; m0 < M; m0 += plan.launch_vectors) {
+        const int64_t mc = std::min(plan.launch_vectors, M - m0);
+        LutPlan sub = plan;
+        sub.batch_tiles = ceil_div(mc, plan.batch_tile);
+        const int rc = launch_lut_once<T>(packed, static_cast<const T *>(x) + m0 * columns,
+                                          static_cast<T *>(y) + m0 * out_width, mc, rows, columns, sub, ws, stream, glu);
+        if (rc != TERNEL_TQ1_OK) return rc;
+    }
+    return TERNEL_TQ1_OK;
+}
+
+template <typename T>
+int launch_lut_once(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
+                    const LutPlan &plan, void *ws, hipStream_t stream, bool glu) {
     const int G = static_cast<int>(columns / kBlockWeights);
     unsigned *counters = plan.k_split > 1 ? static_cast<unsigned *>(ws) : nullptr;
-    float *partial =
-        plan.k_split > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + plan.counter_bytes) : nullptr;
+    uint64_t *partial =
+        plan.k_split > 1 ? reinterpret_cast<uint64_t *>(static_cast<char *>(ws) + plan.counter_bytes) : nullptr;
     if (glu) {  // SwiGLU epilogue: one vector per workgroup
 #define TQ1_LUT_GLU_CASE(CC)                                                                          \
         if (plan.chunk == CC && plan.batch_tile == 1) {                                               \
@@ -2138,9 +2372,9 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
         return fail(TERNEL_TQ1_EINVAL, "k split %d does not divide the tensor's %lld groups per row", k_split,
                     static_cast<long long>(G));
     if (k_split > 65535) return fail(TERNEL_TQ1_EINVAL, "K too large for one launch");
-    if (k_split > 1 && plan->row_blocks > kCounterSlots)
+    if (k_split > 1 && plan->row_blocks > kUsableCounters)
         return fail(TERNEL_TQ1_EINVAL, "%lld row blocks exceed the %d split-K counters",
-                    static_cast<long long>(plan->row_blocks), kCounterSlots);
+                    static_cast<long long>(plan->row_blocks), kUsableCounters);
     plan->k_split = k_split;
     plan->chunk_groups = static_cast<int>(G / k_split);
     const size_t group_bytes = static_cast<size_t>(plan->staged_rows) * kDirectStride * sizeof(_Float16);
@@ -2160,13 +2394,8 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
 template <int NB, int SR>
 int launch_direct_kernel(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int G,
                          const DirectPlan &plan, float *partial, unsigned *counters, hipStream_t stream) {
-    static bool attribute_set = false;  // dynamic LDS above 64 KiB needs the opt-in once per kernel
-    if (!attribute_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&direct_gemm_kernel<NB, SR>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kDirectLdsBytes);
-        if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attribute_set = true;
-    }
+    int rc = ensure_lds_attribute(reinterpret_cast<const void *>(&direct_gemm_kernel<NB, SR>), kDirectLdsBytes);
+    if (rc != TERNEL_TQ1_OK) return rc;
     const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.k_split));
     hipLaunchKernelGGL((direct_gemm_kernel<NB, SR>), grid, dim3(kDirectThreads), plan.lds_bytes, stream, packed,
                        static_cast<const _Float16 *>(x), static_cast<_Float16 *>(y), partial, counters,
@@ -2179,7 +2408,7 @@ int launch_direct(const uint32_t *packed, const void *x, void *y, int64_t M, int
                   const DirectPlan &plan, void *ws, hipStream_t stream) {
     unsigned *counters = plan.k_split > 1 ? static_cast<unsigned *>(ws) : nullptr;
     float *partial =
-        plan.k_split > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes) : nullptr;
+        plan.k_split > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + kPartialOffset) : nullptr;
     const int G = static_cast<int>(columns / kBlockWeights);
     switch (plan.staged_rows) {
         case 8: return launch_direct_kernel<1, 8>(packed, x, y, M, rows, G, plan, partial, counters, stream);
@@ -2241,13 +2470,14 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
     g.tiles_n = static_cast<int>(ceil_div(rows, kWideRows));
     plan->nb = wide_blocks(M, g.tiles_n, g.G, device_cu_count());
     const int64_t tiles = g.tiles_n * ceil_div(M, 32 * plan->nb);
-    static_assert(2 * kWideTileSlots <= kCounterSlots, "two counters per wide tile");
+    static_assert(2 * kWideTileSlots <= kUsableCounters, "two counters per wide tile");
     if (tiles > kWideTileSlots)
         return fail(TERNEL_TQ1_EINVAL, "%lld output tiles exceed the %d stream-K counters", static_cast<long long>(tiles),
                     kWideTileSlots);
     g.tiles = static_cast<int>(tiles);
     g.units = static_cast<int>(tiles * g.G);  // < 2^14 tiles x 2^15 groups
     g.vector_rows = 0;                         // set at launch from the output pointer
+    g.spin_limit = g_spin_limit.load();
     int64_t wgs = device_cu_count();
     if (wgs > g.units) wgs = g.units;
     plan->workgroups = static_cast<int>(wgs);
@@ -2261,14 +2491,9 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
 template <int NB>
 int launch_wide_kernel(const uint32_t *packed, const _Float16 *xp, void *y, float *partial, unsigned *counters,
                        const WideGeometry &geo, int workgroups, hipStream_t stream) {
-    static bool attribute_set = false;  // dynamic LDS above 64 KiB needs the opt-in once
-    if (!attribute_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&wide_gemm_kernel<NB>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 static_cast<int>(wide_lds_bytes(NB)));
-        if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attribute_set = true;
-    }
+    int rc = ensure_lds_attribute(reinterpret_cast<const void *>(&wide_gemm_kernel<NB>),
+                                  static_cast<int>(wide_lds_bytes(NB)));
+    if (rc != TERNEL_TQ1_OK) return rc;
     hipLaunchKernelGGL(wide_gemm_kernel<NB>, dim3(static_cast<unsigned>(workgroups)), dim3(kWideThreads),
                        wide_lds_bytes(NB), stream, packed, xp, static_cast<_Float16 *>(y), partial, counters, geo);
     TQ1_LAUNCH_CHECK();
@@ -2277,8 +2502,8 @@ int launch_wide_kernel(const uint32_t *packed, const _Float16 *xp, void *y, floa
 
 int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &plan, void *ws, hipStream_t stream) {
     unsigned *counters = static_cast<unsigned *>(ws);
-    float *partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes);
-    _Float16 *xp = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kCounterRegionBytes + plan.partial_bytes);
+    float *partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kPartialOffset);
+    _Float16 *xp = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kPartialOffset + plan.partial_bytes);
     const int64_t quads = static_cast<int64_t>(plan.geo.M) * plan.geo.G * 8;  // 32-byte runs of the copy
     hipLaunchKernelGGL(permute_activations_kernel, dim3(static_cast<unsigned>(ceil_div(quads, kThreads))),
                        dim3(kThreads), 0, stream, static_cast<const uint2 *>(x), reinterpret_cast<uint2 *>(xp), quads,
@@ -2389,7 +2614,45 @@ extern "C" {
 
 const char *ternel_tq1_last_error(void) { return g_last_error; }
 
-const char *ternel_tq1_version(void) { return "ternel-tq1-gfx950 0.2.0"; }
+const char *ternel_tq1_version(void) { return "ternel-tq1-gfx950 0.3.0"; }
+
+int ternel_tq1_workspace_error(const void *ws, size_t ws_bytes, int *error, void *stream) {
+    g_last_error[0] = '\0';
+    if (!ws || !error) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if (ws_bytes < kCounterRegionBytes)
+        return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes has no error word", ws_bytes);
+    unsigned word = 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(&word, static_cast<const unsigned *>(ws) + kErrorSlot, sizeof(word),
+                                  hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "reading the workspace error word: %s", hipGetErrorString(e));
+    *error = static_cast<int>(word);
+    return TERNEL_TQ1_OK;
+}
+
+#ifdef TERNEL_TQ1_PROFILE
+// Profile build only: copies (synchronously) and clears the phase stamps of
+// the last stream-GEMV launches; returns the number of waves copied.
+int ternel_tq1_profile_stamps(unsigned long long *host, int64_t max_waves, void *stream) {
+    const int64_t waves = max_waves < kPhaseWaves ? max_waves : kPhaseWaves;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipStreamSynchronize(s);
+    if (e == hipSuccess)
+        e = hipMemcpyFromSymbol(host, HIP_SYMBOL(g_phase_stamps), waves * kPhaseSlots * sizeof(unsigned long long), 0,
+                                hipMemcpyDeviceToHost);
+    static unsigned long long zeros[kPhaseWaves][kPhaseSlots];
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_phase_stamps), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "phase stamps: %s", hipGetErrorString(e));
+    return static_cast<int>(waves);
+}
+#endif
+
+int ternel_tq1_set_spin_limit(int limit) {
+    const int old = g_spin_limit.load();
+    g_spin_limit.store(limit);
+    return old;
+}
 
 int64_t ternel_tq1_packed_words(int64_t rows, int64_t columns) {
     if (rows <= 0 || columns <= 0 || columns % kBlockWeights) return 0;
@@ -2465,6 +2728,50 @@ int ternel_tq1_interleave(const uint8_t *blocks, int64_t rows, int64_t columns, 
     return TERNEL_TQ1_OK;
 }
 
+static int check_tiled(int64_t rows, int64_t columns, int64_t tile) {
+    int rc;
+    if ((rc = check_geometry(1, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if (tile <= 0 || rows % tile)
+        return fail(TERNEL_TQ1_EINVAL, "tile %lld does not divide the tensor's %lld rows", static_cast<long long>(tile),
+                    static_cast<long long>(rows));
+    return TERNEL_TQ1_OK;
+}
+
+int ternel_tq1_words_from_tiled(const uint8_t *codes, const uint16_t *scales, int64_t rows, int64_t columns,
+                                int64_t tile, uint32_t *packed, uint64_t *counters, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_tiled(rows, columns, tile)) != TERNEL_TQ1_OK) return rc;
+    if (!codes || !scales || !packed || !counters) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(scales) & 1u) || (reinterpret_cast<uintptr_t>(packed) & 3u))
+        return fail(TERNEL_TQ1_EINVAL, "scales must be 2-byte and packed words 4-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto *cnt = reinterpret_cast<unsigned long long *>(counters);
+    hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(64), 0, s, cnt, 2);
+    TQ1_LAUNCH_CHECK();
+    const int64_t total = packed_words(rows, columns);
+    hipLaunchKernelGGL(words_from_tiled_kernel, dim3(static_cast<unsigned>(ceil_div(total, kThreads))), dim3(kThreads),
+                       0, s, codes, scales, packed, rows, columns / kBlockWeights, tile, total, cnt);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
+int ternel_tq1_tiled_from_words(const uint32_t *packed, int64_t rows, int64_t columns, int64_t tile, uint8_t *codes,
+                                uint16_t *scales, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_tiled(rows, columns, tile)) != TERNEL_TQ1_OK) return rc;
+    if (!codes || !scales || !packed) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(scales) & 1u) || (reinterpret_cast<uintptr_t>(packed) & 3u))
+        return fail(TERNEL_TQ1_EINVAL, "scales must be 2-byte and packed words 4-byte aligned");
+    const int64_t total = packed_words(rows, columns);
+    hipLaunchKernelGGL(tiled_from_words_kernel, dim3(static_cast<unsigned>(ceil_div(total, kThreads))), dim3(kThreads),
+                       0, static_cast<hipStream_t>(stream), packed, codes, scales, rows, columns / kBlockWeights, tile,
+                       total);
+    TQ1_LAUNCH_CHECK();
+    return TERNEL_TQ1_OK;
+}
+
 int ternel_tq1_deinterleave(const uint32_t *packed, int64_t rows, int64_t columns, uint8_t *blocks, void *stream) {
     g_last_error[0] = '\0';
     int rc;
@@ -2497,7 +2804,6 @@ int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M,
     if ((rc = plan_lut(M, rows, columns, batch_tile, k_split, &plan)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
     if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
-    if (plan.batch_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");
     const size_t need = plan.counter_bytes + plan.partial_bytes;
     if (need && (!ws || ws_bytes < need))
         return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
@@ -2519,17 +2825,17 @@ size_t ternel_tq1_gemm_workspace_bytes(int64_t M, int64_t rows, int64_t columns,
     if (form == TERNEL_TQ1_GEMM_DIRECT) {
         DirectPlan direct;
         if (plan_direct(M, rows, columns, k_split, &direct) != TERNEL_TQ1_OK) return 0;
-        return direct.k_split > 1 ? kCounterRegionBytes + direct.partial_bytes : 0;
+        return direct.k_split > 1 ? kPartialOffset + direct.partial_bytes : 0;
     }
     if (form == TERNEL_TQ1_GEMM_WIDE) {
         WidePlan wide;
         if (plan_wide(M, rows, columns, k_split, &wide) != TERNEL_TQ1_OK) return 0;
-        return kCounterRegionBytes + wide.partial_bytes + wide.xp_bytes;
+        return kPartialOffset + wide.partial_bytes + wide.xp_bytes;
     }
     if (form != TERNEL_TQ1_GEMM_TILE) return 0;
     GemmPlan plan;
     if (plan_gemm(M, rows, columns, k_split, &plan) != TERNEL_TQ1_OK) return 0;
-    return plan.k_split > 1 ? kCounterRegionBytes + static_cast<size_t>(plan.k_split) * M * rows * sizeof(float)
+    return plan.k_split > 1 ? kPartialOffset + static_cast<size_t>(plan.k_split) * M * rows * sizeof(float)
                             : 0;
 }
 
@@ -2550,7 +2856,7 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
         if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
         if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
         if (reinterpret_cast<uintptr_t>(x) & 7u) return fail(TERNEL_TQ1_EINVAL, "activations must be 8-byte aligned");
-        const size_t need = direct.k_split > 1 ? kCounterRegionBytes + direct.partial_bytes : 0;
+        const size_t need = direct.k_split > 1 ? kPartialOffset + direct.partial_bytes : 0;
         if (need && (!ws || ws_bytes < need))
             return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
                         need);
@@ -2562,7 +2868,7 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
         if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
         if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
         if (reinterpret_cast<uintptr_t>(x) & 15u) return fail(TERNEL_TQ1_EINVAL, "activations must be 16-byte aligned");
-        const size_t need = kCounterRegionBytes + wide.partial_bytes + wide.xp_bytes;
+        const size_t need = kPartialOffset + wide.partial_bytes + wide.xp_bytes;
         if (!ws || ws_bytes < need)
             return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
                         need);
@@ -2576,11 +2882,11 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
     float *partial = nullptr;
     if (plan.k_split > 1) {
         // Partials go past the counter region, which stays untouched (and zero).
-        const size_t need = kCounterRegionBytes + static_cast<size_t>(plan.k_split) * M * rows * sizeof(float);
+        const size_t need = kPartialOffset + static_cast<size_t>(plan.k_split) * M * rows * sizeof(float);
         if (!ws || ws_bytes < need)
             return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
                         need);
-        partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kCounterRegionBytes);
+        partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kPartialOffset);
     }
     return launch_gemm(packed, x, y, M, rows, columns, plan, partial, static_cast<hipStream_t>(stream));
 }
@@ -2616,7 +2922,7 @@ int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M,
 // expects to find zero.
 static size_t swiglu_pairs_offset(int64_t M, int64_t rows, int64_t columns) {
     const size_t gemm = ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
-    return (std::max(gemm, kCounterRegionBytes) + 255) / 256 * 256;
+    return (std::max(gemm, kPartialOffset) + 255) / 256 * 256;
 }
 
 int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype) {
@@ -2650,7 +2956,6 @@ int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M,
     if (linear_uses_lut(M, rows, columns, dtype)) {
         LutPlan plan;
         if ((rc = plan_lut(M, rows, columns, 1, 0, &plan)) != TERNEL_TQ1_OK) return rc;
-        if (plan.batch_tiles > 65535) return fail(TERNEL_TQ1_EINVAL, "batch too large for one launch");
         const size_t need = plan.counter_bytes + plan.partial_bytes;
         if (need && (!ws || ws_bytes < need))
             return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,

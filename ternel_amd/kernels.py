@@ -1,28 +1,40 @@
 """Functional entry points over the gfx950 library (mirror of src/ternel_mlx/kernels.py:951-1398).
 
-``tq1_matmul`` (LUT23: decode GEMV and small batches), ``tq1_gemm`` (MFMA:
-prefill) and ``tq1_get_rows`` (embedding gather) take the *packed* device
-weight -- the canonical 28-byte blocks permuted into 64-row word-interleaved
-tiles, a uint32 tensor of shape ``(ceil(rows/64), groups_per_row, 7, 64)`` made
-by :func:`pack_weights` -- check every argument on the host and raise
-``FormatError`` before anything is launched, as the reference's wrappers do
-(``_check_packed``/``_check_activations``, kernels.py:1191-1212, 1274-1284).
-Outputs are fresh tensors in the activation dtype.
+Two surfaces over the same kernels:
 
-Split-K workspaces: the LUT23 kernel reduces its K chunks inside the launch
-through arrival counters that must start at zero and are left at zero, so the
-workspace is allocated zero-filled once per device and reused.
+* the reference's own signatures -- ``tq1_matmul(codes, scales, x, *,
+  groups_per_row, tile, config)``, ``tq1_gemm(...)`` and ``tq1_get_rows(codes,
+  scales, indices, *, groups_per_row, tile, dtype, threads, safe_clamp)`` --
+  over the reference's tiled pair (``codes`` uint8 ``(tiles, G, 26, tile)``,
+  ``scales`` uint16 raw fp16 bits ``(tiles, G, tile)``) as device tensors. The
+  pair is converted once, on the GPU, into the engine's packed words and the
+  result cached for as long as both tensors live unchanged (their storage and
+  version counters key the cache), so repeated calls pay nothing for it;
+* the engine's own ``*_words`` functions over packed words (``pack_weights``),
+  which the modules use.
+
+Every argument is checked on the host and ``FormatError`` raised before
+anything is launched, with the reference's messages (``_check_packed`` /
+``_check_activations``, kernels.py:1191-1212, 1274-1284). Outputs are fresh
+tensors in the activation dtype.
+
+Split-K workspaces: kernels that reduce K chunks inside the launch use arrival
+counters and piece slots that start at zero and are left at zero, so each
+(device, stream) gets one zero-filled workspace, reused.
 """
 
 from __future__ import annotations
 
+import ctypes
 import math
+import weakref
+from collections import OrderedDict
 from dataclasses import dataclass
 
 import torch
 
 from . import _lib
-from .format import BLOCK_BYTES, FormatError, as_device_blocks
+from .format import BLOCK_BYTES, BLOCK_SIZE, CODE_SLOTS, FormatError, as_device_blocks
 from .layout import PackedTensorLayout
 
 ACTIVATION_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
@@ -36,16 +48,29 @@ LUT23_BATCH_TILES = (1, 2, 4)
 
 @dataclass(frozen=True)
 class MatmulConfig:
-    """LUT23 knobs (src/ternel_mlx/kernels.py:963-1006): batch tile and K split.
+    """LUT23 knobs, with the reference's fields (src/ternel_mlx/kernels.py:963-1006).
 
-    ``0`` means automatic: a batch tile of 1 (fastest at every measured 27B
-    shape) and the split measured best for the shape's groups per row.
+    ``batch_tile`` (1, 2 or 4 vectors per workgroup) and ``k_split`` (K chunks,
+    dividing the groups per row, reduced in chunk order) are honoured; ``0``
+    means automatic for both -- one vector per workgroup and the split measured
+    best for the shape, and at M = 1 the stream GEMV. ``threads``,
+    ``padded_lut`` and ``safe_clamp`` are the Metal kernel's own template knobs:
+    they are validated as the reference validates them and otherwise have no
+    effect (the gfx950 kernels fix their workgroup sizes, keep one table layout
+    and clamp every table index, so they stay memory-safe on illegal bytes).
+    Fields keep the reference's order, so positional construction means the
+    same thing.
     """
 
+    threads: int = LUT23_THREADS
     batch_tile: int = 0
+    padded_lut: bool = False
+    safe_clamp: bool = False
     k_split: int = 0
 
     def __post_init__(self) -> None:
+        if self.threads <= 0 or self.threads % 32:
+            raise FormatError(f"threads must be a positive multiple of the 32-wide simdgroup, got {self.threads}")
         if self.batch_tile not in (0, *LUT23_BATCH_TILES):
             raise FormatError(f"batch tile must be one of {LUT23_BATCH_TILES}, got {self.batch_tile}")
         if self.k_split < 0:
@@ -75,16 +100,38 @@ class GemmConfig:
     when it has enough tiles (CUs/4) or work per CU (15 steps) for its stream-K
     reduction to pay, ``"tile"`` otherwise (and whenever a K split above 1 is
     fixed).
+
+    The reference's tiling fields (``batch_block`` .. ``safe_clamp``) are
+    accepted by keyword so its configurations construct unchanged; they tile
+    Apple's 8x8 simdgroup matrices and have no meaning for CDNA4's MFMA, except
+    ``direct_fragments``: set (with ``form`` left automatic) it selects the
+    direct-fragment form for batches it can hold.
     """
 
     k_split: int = 0
     form: str = "auto"
+    batch_block: int | None = None
+    row_block: int | None = None
+    k_block: int | None = None
+    simd_rows: int | None = None
+    simd_columns: int | None = None
+    direct_fragments: bool | None = None
+    direct_epilogue: bool | None = None
+    threadgroup_table: bool | None = None
+    safe_clamp: bool = False
 
     def __post_init__(self) -> None:
         if self.k_split < 0:
             raise FormatError(f"k split must be positive, got {self.k_split}")
         if self.form not in GEMM_FORMS:
             raise FormatError(f"GEMM form must be one of {sorted(GEMM_FORMS)}, got {self.form!r}")
+        if self.threadgroup_table and not self.direct_fragments:
+            raise FormatError("a threadgroup trit table is only read by the direct-fragment form")
+
+    def form_for(self, batch: int) -> str:
+        if self.form == "auto" and self.direct_fragments and batch <= DIRECT_MAX_BATCH:
+            return "direct"
+        return self.form
 
     @property
     def benchmark_name(self) -> str:
@@ -152,37 +199,85 @@ def check_activations(x: torch.Tensor, *, layout: PackedTensorLayout) -> int:
     return x.shape[0]
 
 
-_WORKSPACES: dict[int, torch.Tensor] = {}
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+# Workspaces that a graph may still address: replaced by a larger one after
+# their stream was captured, so never freed (a replay would otherwise write
+# counters and partials into memory the caching allocator has reused).
+_RETIRED: list[torch.Tensor] = []
+_CAPTURED: set[tuple[int, int]] = set()
+
+
+def _workspace_key(device: torch.device) -> tuple[int, int]:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return index, torch.cuda.current_stream(torch.device("cuda", index)).cuda_stream
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Zero-initialised split-K scratch, one per device, grown on demand.
+    """Zero-initialised split-K scratch, one per (device, stream), grown on demand.
 
-    The LUT23 kernel leaves its arrival counters at zero after every launch, so
-    the buffer only needs zeroing when it is created -- which never happens
-    inside a graph capture once an eager call of the same size has run. Calls
-    sharing the buffer must not run concurrently (one stream per device).
+    The kernels leave their counters and piece slots zero after every launch,
+    so a buffer only needs zeroing when it is created -- never inside a graph
+    capture: size it with an eager call of the same shape first. Calls on one
+    stream run in order, so they can share its buffer; calls on two streams
+    get two buffers and never race on each other's counters.
     """
     if nbytes == 0:
         return None
-    key = device.index if device.index is not None else torch.cuda.current_device()
+    key = _workspace_key(device)
+    capturing = torch.cuda.is_current_stream_capturing()
     buf = _WORKSPACES.get(key)
-    if buf is None or buf.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
+    if capturing and (buf is None or buf.numel() < nbytes):
+        # A capture stream (torch.cuda.graph captures on a side stream) borrows
+        # the device's largest eager workspace: replays then share it with that
+        # stream's eager calls, which must not run at the same time.
+        sized = [k for k, b in _WORKSPACES.items() if k[0] == key[0] and b.numel() >= nbytes]
+        if not sized:
             raise RuntimeError("split-K workspace must be sized by an eager call before graph capture")
-        buf = torch.zeros(max(nbytes, 1 << 22), dtype=torch.uint8, device=device)
-        torch.cuda.synchronize(device)
-        _WORKSPACES[key] = buf
+        key = max(sized, key=lambda k: _WORKSPACES[k].numel())
+        buf = _WORKSPACES[key]
+    if buf is None or buf.numel() < nbytes:
+        new = torch.zeros(max(nbytes, 1 << 22), dtype=torch.uint8, device=torch.device("cuda", key[0]))
+        torch.cuda.synchronize(key[0])
+        if buf is not None and key in _CAPTURED:
+            _RETIRED.append(buf)
+        _WORKSPACES[key] = buf = new
+    if capturing:
+        _CAPTURED.add(key)
     return buf
 
 
-def tq1_matmul(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
-               config: MatmulConfig | None = None) -> torch.Tensor:
-    """``x @ W.T`` through the LUT23 kernel; ``(batch, rows)`` in ``x.dtype``.
+def workspace_errors() -> dict[tuple[int, int], int]:
+    """The error word of every workspace (synchronises each one's stream): a
+    nonzero word names the kernels whose bounded wait for another workgroup's
+    partial gave up (1 = the M=1 stream GEMV, 2 = the wide GEMM)."""
+    handle = _lib.lib()
+    words = {}
+    for (index, stream), buf in _WORKSPACES.items():
+        word = ctypes.c_int(0)
+        with torch.cuda.device(index):
+            _lib.check(handle.ternel_tq1_workspace_error(buf.data_ptr(), buf.numel(), ctypes.byref(word), stream))
+        words[(index, stream)] = word.value
+    return words
 
-    Reference: tq1_matmul, src/ternel_mlx/kernels.py:1215-1271. A ``k_split`` that
-    does not divide the group count is refused, as there.
-    """
+
+def check_workspaces() -> None:
+    """Raise ``NativeError`` if any workspace reports a wait that gave up. The
+    workspace is zeroed again first (its counters may be left set), so the
+    next call starts clean."""
+    failed = {key: word for key, word in workspace_errors().items() if word}
+    for key in failed:
+        _WORKSPACES[key].zero_()
+    if failed:
+        torch.cuda.synchronize()
+        raise _lib.NativeError(f"a kernel's bounded wait for a published partial gave up: {failed}")
+
+
+def tq1_matmul_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
+                     config: MatmulConfig | None = None) -> torch.Tensor:
+    """``x @ W.T`` through the LUT23 kernels (at M = 1 with automatic knobs the
+    stream GEMV); ``(batch, rows)`` in ``x.dtype``. A ``k_split`` that does not
+    divide the group count is refused, as the reference refuses it
+    (src/ternel_mlx/kernels.py:1240-1246)."""
     config = config or MatmulConfig()
     check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
@@ -203,21 +298,27 @@ def tq1_matmul(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLay
     return out
 
 
-def tq1_gemm(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
-             config: GemmConfig | None = None) -> torch.Tensor:
-    """``x @ W.T`` on the MFMA kernel (fp16 activations); reference tq1_gemm, kernels.py:1287-1357."""
+def tq1_gemm_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
+                   config: GemmConfig | None = None) -> torch.Tensor:
+    """``x @ W.T`` on the MFMA kernels (reference tq1_gemm, kernels.py:1287-1357).
+
+    The matrix cores take fp16 activations (the graded type; weights are exact
+    in fp16). bf16 and fp32 activations -- whose range or precision fp16 would
+    not hold -- run through the LUT23 kernel, which computes in fp32 from the
+    activations as given, in as many launches as its counters need."""
     config = config or GemmConfig()
     check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
-    if x.dtype != torch.float16:
-        raise FormatError(f"the MFMA path takes float16 activations, got {x.dtype}")
     if config.k_split and layout.groups_per_row % config.k_split:
         raise FormatError(
             f"k split {config.k_split} does not divide the tensor's {layout.groups_per_row} groups per row"
         )
-    if config.form == "direct" and batch > DIRECT_MAX_BATCH:
+    if x.dtype != torch.float16:
+        return tq1_matmul_words(packed, x, layout=layout, config=MatmulConfig(batch_tile=1, k_split=config.k_split))
+    form_name = config.form_for(batch)
+    if form_name == "direct" and batch > DIRECT_MAX_BATCH:
         raise FormatError(f"the direct-fragment form takes at most {DIRECT_MAX_BATCH} activation rows, got {batch}")
-    form = GEMM_FORMS[config.form]
+    form = GEMM_FORMS[form_name]
     x = x.contiguous()
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
@@ -230,7 +331,7 @@ def tq1_gemm(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayou
     return out
 
 
-def tq1_linear(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+def tq1_linear_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
     """The library's own dispatch (``ternel_tq1_linear``) for a 2-D ``x``."""
     check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
@@ -246,7 +347,7 @@ def tq1_linear(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLay
     return out
 
 
-def tq1_swiglu(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+def tq1_swiglu_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
     """SiLU(gate) * up of a SwiGLU MLP whose gate and up projections are one
     packed weight with alternating rows (``layout.interleave_gate_up``):
     ``(batch, rows // 2)`` in ``x.dtype``, each gate/up value rounded to
@@ -275,17 +376,16 @@ def _gather_ids(indices: torch.Tensor, dtype: torch.dtype, device) -> torch.Tens
         raise FormatError(f"indices must be 1-D, got shape {tuple(indices.shape)}")
     if indices.numel() <= 0:
         raise FormatError("indices are empty")
-    if indices.dtype not in (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8):
+    if indices.dtype not in (torch.int8, torch.int16, torch.int32, torch.int64, torch.uint8, torch.uint32):
         raise FormatError(f"indices must be an integer tensor, got {indices.dtype}")
     return indices.to(device=device, dtype=torch.int64).contiguous()
 
 
-def tq1_get_rows(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
-                 dtype: torch.dtype) -> torch.Tensor:
-    """Decode the rows named by ``indices`` (1-D); reference tq1_get_rows, kernels.py:1360-1398.
-
-    Ids outside ``[0, rows)`` read as zeros, as the reference kernel does.
-    """
+def tq1_get_rows_words(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
+                       dtype: torch.dtype) -> torch.Tensor:
+    """Decode the rows named by ``indices`` (1-D) from packed words; ids outside
+    ``[0, rows)`` read as zeros, as the reference kernel does
+    (src/ternel_mlx/kernels.py:869-880)."""
     check_packed(packed, layout=layout)
     ids = _gather_ids(indices, dtype, packed.device)
     out = torch.empty((ids.numel(), layout.columns), dtype=dtype, device=packed.device)
@@ -297,7 +397,7 @@ def tq1_get_rows(packed: torch.Tensor, indices: torch.Tensor, *, layout: PackedT
 
 def tq1_get_rows_canonical(blocks: torch.Tensor, indices: torch.Tensor, *, layout: PackedTensorLayout,
                            dtype: torch.dtype) -> torch.Tensor:
-    """``tq1_get_rows`` over canonical ``(rows, G, 28)`` uint8 device blocks (``unpack_weights``):
+    """Row gather over canonical ``(rows, G, 28)`` uint8 device blocks (``unpack_weights``):
     a token's blocks are one contiguous run, so a gather reads only the rows it returns."""
     if blocks.dtype != torch.uint8 or tuple(blocks.shape) != tuple(layout.canonical_shape):
         raise FormatError(f"canonical blocks must be uint8 {tuple(layout.canonical_shape)}, "
@@ -312,17 +412,187 @@ def tq1_get_rows_canonical(blocks: torch.Tensor, indices: torch.Tensor, *, layou
     return out
 
 
+# ---------------------------------------------------------------------------
+# The reference's tiled pair (codes, scales) on the device
+# ---------------------------------------------------------------------------
+SCALE_DTYPES = (torch.uint16, torch.int16)
+
+
+def _check_tiled(codes, scales, *, groups_per_row: int, tile: int) -> int:
+    """src/ternel_mlx/kernels.py:1191-1212 (same messages), for device tensors."""
+    if not isinstance(codes, torch.Tensor) or not isinstance(scales, torch.Tensor):
+        raise FormatError("codes and scales must be torch tensors")
+    if codes.dtype != torch.uint8:
+        raise FormatError(f"codes must be uint8, got {codes.dtype}")
+    if scales.dtype not in SCALE_DTYPES:
+        raise FormatError(f"scales must be uint16 of raw FP16 bits, got {scales.dtype}")
+    if groups_per_row <= 0:
+        raise FormatError(f"groups per row must be positive, got {groups_per_row}")
+    if tile <= 0:
+        raise FormatError(f"tile must be positive, got {tile}")
+    if codes.ndim != 4 or tuple(codes.shape[1:]) != (groups_per_row, CODE_SLOTS, tile):
+        raise FormatError(
+            f"codes shape {tuple(codes.shape)} does not match (tiles, {groups_per_row}, {CODE_SLOTS}, {tile})"
+        )
+    tiles = codes.shape[0]
+    if tuple(scales.shape) != (tiles, groups_per_row, tile):
+        raise FormatError(f"scales shape {tuple(scales.shape)} does not match ({tiles}, {groups_per_row}, {tile})")
+    if tiles <= 0:
+        raise FormatError("packed tensor has no tiles")
+    if not codes.is_cuda or not scales.is_cuda or codes.device != scales.device:
+        raise FormatError("codes and scales must live on the same GPU")
+    return tiles
+
+
+def _tiled_layout(codes, scales, *, groups_per_row: int, tile: int) -> PackedTensorLayout:
+    tiles = _check_tiled(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    return PackedTensorLayout(rows=tiles * tile, columns=groups_per_row * BLOCK_SIZE, tile=tile)
+
+
+def words_from_tiled(codes: torch.Tensor, scales: torch.Tensor, *, layout: PackedTensorLayout,
+                     validate: bool = True) -> torch.Tensor:
+    """The tiled pair -> packed words on the GPU (exact), scanning every code
+    byte on the way; raises the reference's ``validate_packed_codes`` error
+    (src/ternel_mlx/packing.py:29-48) when any is out of range."""
+    _check_tiled(codes, scales, groups_per_row=layout.groups_per_row, tile=layout.tile)
+    codes = codes.contiguous()
+    scales = scales.contiguous()
+    packed = torch.empty(packed_shape(layout), dtype=torch.int32, device=codes.device)
+    counters = torch.empty(2, dtype=torch.int64, device=codes.device)
+    _lib.check(_lib.lib().ternel_tq1_words_from_tiled(
+        codes.data_ptr(), scales.data_ptr(), layout.rows, layout.columns, layout.tile, packed.data_ptr(),
+        counters.data_ptr(), _stream(codes.device)))
+    if validate:
+        regular, tail = (int(v) for v in counters.cpu())
+        if regular or tail:
+            from .format import MAX_FULL_CODE_BYTE, MAX_TAIL_CODE_BYTE
+
+            raise FormatError(
+                f"packed codes contain out-of-range base-3 bytes: regular={regular} "
+                f"(max {MAX_FULL_CODE_BYTE}), tail={tail} (max {MAX_TAIL_CODE_BYTE})"
+            )
+    return packed
+
+
+def tiled_from_words(packed: torch.Tensor, *, layout: PackedTensorLayout) -> tuple[torch.Tensor, torch.Tensor]:
+    """Packed words -> the reference's ``(codes, scales)`` device tensors (exact)."""
+    check_packed(packed, layout=layout)
+    codes = torch.empty(layout.codes_shape, dtype=torch.uint8, device=packed.device)
+    scales = torch.empty(layout.scales_shape, dtype=torch.uint16, device=packed.device)
+    _lib.check(_lib.lib().ternel_tq1_tiled_from_words(
+        packed.data_ptr(), layout.rows, layout.columns, layout.tile, codes.data_ptr(), scales.data_ptr(),
+        _stream(packed.device)))
+    return codes, scales
+
+
+# Packed words of (codes, scales) pairs the functional calls have seen, keyed by
+# the pair's identity and checked against their storage and version counters
+# on every hit; least recently used first, at most this many.
+WORD_CACHE_ENTRIES = 1024
+_WORD_CACHE: OrderedDict[tuple[int, int], tuple] = OrderedDict()
+
+
+def words_of(codes: torch.Tensor, scales: torch.Tensor, *, groups_per_row: int, tile: int) -> tuple[
+        torch.Tensor, PackedTensorLayout]:
+    """Packed words (and layout) for the tiled pair, converted once and cached
+    while both tensors live unchanged -- an in-place write bumps a tensor's
+    version and forces a new conversion."""
+    layout = _tiled_layout(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    key = (id(codes), id(scales))
+    stamp = (codes.data_ptr(), codes._version, scales.data_ptr(), scales._version, layout)
+    hit = _WORD_CACHE.get(key)
+    if hit is not None:
+        ref_codes, ref_scales, hit_stamp, packed = hit
+        if ref_codes() is codes and ref_scales() is scales and hit_stamp == stamp:
+            _WORD_CACHE.move_to_end(key)
+            return packed, layout
+    packed = words_from_tiled(codes, scales, layout=layout)
+    _WORD_CACHE[key] = (weakref.ref(codes), weakref.ref(scales), stamp, packed)
+    _WORD_CACHE.move_to_end(key)
+    while len(_WORD_CACHE) > WORD_CACHE_ENTRIES:
+        _WORD_CACHE.popitem(last=False)
+    return packed, layout
+
+
+def _check_activation_width(x: torch.Tensor, *, groups_per_row: int) -> None:
+    """src/ternel_mlx/kernels.py:1274-1284, same messages."""
+    if x.dtype not in ACTIVATION_DTYPES:
+        raise FormatError(f"activations must be one of {ACTIVATION_DTYPES}, got {x.dtype}")
+    if x.ndim != 2:
+        raise FormatError(f"activations must be 2-D (batch, columns), got shape {tuple(x.shape)}")
+    columns = groups_per_row * BLOCK_SIZE
+    if x.shape[1] != columns:
+        raise FormatError(f"activations have {x.shape[1]} columns, expected {columns}")
+    if x.shape[0] <= 0:
+        raise FormatError("activations have an empty batch dimension")
+
+
+def tq1_matmul(codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, *, groups_per_row: int, tile: int,
+               config: MatmulConfig | None = None) -> torch.Tensor:
+    """``x @ W.T`` for a TQ1_G128 packed ``W`` of shape ``(tiles * tile,
+    groups_per_row * 128)`` -- the reference's signature and checks
+    (src/ternel_mlx/kernels.py:1215-1271). ``x`` is 2-D ``(batch, columns)``;
+    the result ``(batch, rows)`` in ``x``'s dtype."""
+    config = config or MatmulConfig()
+    _check_tiled(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    _check_activation_width(x, groups_per_row=groups_per_row)
+    if config.k_split and groups_per_row % config.k_split:
+        raise FormatError(f"k split {config.k_split} does not divide the tensor's {groups_per_row} groups per row")
+    packed, layout = words_of(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    return tq1_matmul_words(packed, x, layout=layout, config=config)
+
+
+def tq1_gemm(codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, *, groups_per_row: int, tile: int,
+             config: GemmConfig | None = None) -> torch.Tensor:
+    """``x @ W.T`` on the matrix cores -- the reference's signature
+    (src/ternel_mlx/kernels.py:1287-1357); see ``tq1_gemm_words``."""
+    config = config or GemmConfig()
+    _check_tiled(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    _check_activation_width(x, groups_per_row=groups_per_row)
+    packed, layout = words_of(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    return tq1_gemm_words(packed, x, layout=layout, config=config)
+
+
+def tq1_get_rows(codes: torch.Tensor, scales: torch.Tensor, indices: torch.Tensor, *, groups_per_row: int,
+                 tile: int, dtype: torch.dtype, threads: int = 256, safe_clamp: bool = False) -> torch.Tensor:
+    """Decode the rows named by ``indices`` out of a packed embedding table --
+    the reference's signature and checks (src/ternel_mlx/kernels.py:1360-1398).
+    ``threads`` is validated as there; ``safe_clamp`` is accepted and has no
+    effect (the gather kernel bounds every table access and reads ids outside
+    the table as zero rows either way)."""
+    _check_tiled(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    if dtype not in ACTIVATION_DTYPES:
+        raise FormatError(f"output dtype must be one of {ACTIVATION_DTYPES}, got {dtype}")
+    if indices.ndim != 1:
+        raise FormatError(f"indices must be 1-D, got shape {tuple(indices.shape)}")
+    if indices.numel() <= 0:
+        raise FormatError("indices are empty")
+    if threads <= 0 or threads % 32:
+        raise FormatError(f"threads must be a positive multiple of 32, got {threads}")
+    packed, layout = words_of(codes, scales, groups_per_row=groups_per_row, tile=tile)
+    return tq1_get_rows_words(packed, indices, layout=layout, dtype=dtype)
+
+
 __all__ = [
     "ACTIVATION_DTYPES",
     "BLOCK_BYTES",
     "GemmConfig",
     "MatmulConfig",
+    "check_workspaces",
     "pack_weights",
     "packed_shape",
+    "tiled_from_words",
     "tq1_gemm",
+    "tq1_gemm_words",
     "tq1_get_rows",
     "tq1_get_rows_canonical",
-    "tq1_linear",
+    "tq1_get_rows_words",
+    "tq1_linear_words",
     "tq1_matmul",
+    "tq1_matmul_words",
+    "tq1_swiglu_words",
     "unpack_weights",
+    "words_from_tiled",
+    "words_of",
+    "workspace_errors",
 ]

@@ -1,13 +1,21 @@
-"""Tensor geometry and the two byte layouts of a packed TQ1_G128 weight.
+"""Tensor geometry and the byte layouts of a packed TQ1_G128 weight.
 
 ``PackedTensorLayout`` keeps the reference's API (src/ternel_mlx/layout.py:41-148):
-same fields, properties, messages and JSON. The device layout of this engine is
-the *canonical* one -- ``(rows, groups_per_row, 28)`` contiguous blocks, the
-bytes ``decode_tq1_blocks`` takes -- because the gfx950 kernels stream whole
-28-byte blocks. The reference's MLX artifact stores the same bytes permuted
-into ``codes[tile][group][slot][row_in_tile]`` + ``scales[tile][group][row_in_tile]``;
-``pack_blocks``/``unpack_blocks`` convert between the two exactly, on the host
-at load time, as src/ternel_mlx/packing.py:51-83 does.
+same fields, properties, messages and JSON. Three arrangements of the same
+28 bytes per 128 weights exist:
+
+* *canonical* blocks, ``(rows, groups_per_row, 28)`` contiguous -- the bytes
+  ``decode_tq1_blocks`` takes and the sidecar stores;
+* the reference's *tiled pair* -- ``codes[tile][group][slot][row_in_tile]`` and
+  ``scales[tile][group][row_in_tile]`` -- the MLX artifact's arrays and the
+  state of its modules; ``pack_blocks``/``unpack_blocks`` convert it on the
+  host as src/ternel_mlx/packing.py:51-83 does, ``kernels.words_from_tiled`` /
+  ``tiled_from_words`` on the GPU;
+* the engine's *packed words* -- what the gfx950 kernels stream: the canonical
+  blocks permuted at 4-byte granularity into 64-row tiles, word j of block
+  (r, g) at ``packed[r // 64][g][j][r % 64]`` (uint32), rows past the end zero,
+  so one wave64 reads one word of 64 rows' blocks with one coalesced 256-byte
+  load (``kernels.pack_weights`` / ``unpack_weights``).
 """
 
 from __future__ import annotations
@@ -20,7 +28,7 @@ from .format import BLOCK_BYTES, BLOCK_SIZE, CODE_SLOTS, FormatError
 
 LAYOUT_VERSION = 1
 LAYOUT_NAME = "TQ1_G128_MLX_TILED"
-DEVICE_LAYOUT_NAME = "TQ1_G128_CANONICAL_ROW_MAJOR"
+DEVICE_LAYOUT_NAME = "TQ1_G128_WORDS_64_ROW_INTERLEAVED"
 PREFERRED_TILE = 256
 SCALE_BYTES = BLOCK_BYTES - CODE_SLOTS
 CODES_SUFFIX = "codes"

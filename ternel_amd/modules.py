@@ -1,14 +1,19 @@
 """torch modules that execute packed TQ1_G128 weights without unpacking them.
 
 Twins of the reference's module API (src/ternel_mlx/modules.py:425-549):
-``packed_matmul``, ``PackedLinear`` and ``PackedEmbedding`` keep their names,
-constructor arguments, call signatures, output shapes/dtypes and FormatError
-messages. The only parameter a module owns is its packed weight -- here the
-``packed`` buffer: the canonical 28-byte blocks permuted into 64-row
-word-interleaved tiles, the exact words the gfx950 kernels stream. Canonical
-blocks (``load_blocks``) and the reference's tiled ``codes``/``scales`` pair
-(``load_packed``/``load_weights``) are accepted on load and exposed as
-properties, all by exact permutation.
+``packed_matmul(codes, scales, x, *, layout)``, ``PackedLinear`` and
+``PackedEmbedding`` keep their names, constructor arguments, call signatures,
+output shapes/dtypes and FormatError messages, and their state is the
+reference's: ``codes`` (uint8 ``(tiles, G, 26, tile)``) and ``scales`` (uint16
+raw fp16 bits ``(tiles, G, tile)``) -- the state-dict keys the MLX artifact
+uses (src/ternel_mlx/layout.py:37-38), loadable with ``load_state_dict`` or
+``load_weights([("codes", c), ("scales", s)])``.
+
+What the modules keep in device memory is one copy of the weight, as the
+engine's packed words (the same 28 bytes per 128 weights, permuted at 4-byte
+granularity for the gfx950 kernels). ``codes`` and ``scales`` read back as
+device tensors, derived from the words once per weight version on the GPU;
+assigning either converts on the GPU (with the fail-closed byte scan).
 
 ``replace_with_packed`` is the torch counterpart of
 src/ternel_mlx/packed_model.py:72-92: it swaps every bias-free ``nn.Linear`` and
@@ -27,17 +32,20 @@ from .kernels import (
     MatmulConfig,
     pack_weights,
     packed_shape,
-    tq1_gemm,
-    tq1_get_rows,
+    tiled_from_words,
+    tq1_gemm_words,
     tq1_get_rows_canonical,
-    tq1_matmul,
-    tq1_swiglu,
+    tq1_get_rows_words,
+    tq1_matmul_words,
+    tq1_swiglu_words,
     unpack_weights,
+    words_from_tiled,
+    words_of,
 )
-from .layout import PackedTensorLayout, interleave_gate_up, pack_blocks, unpack_blocks
+from .layout import PackedTensorLayout, interleave_gate_up, unpack_blocks
 
 # Dispatch (src/ternel_mlx/modules.py:331-422, re-measured for MI355X): the
-# LUT23 kernel for small batches, the MFMA kernels above them. The LUT kernel's
+# LUT23 kernels for small batches, the MFMA kernels above them. The LUT kernel's
 # cost grows linearly with the batch (one table set per vector) while its bytes
 # do not, so it only pays while the weight stream dominates. The rule lives in
 # the library (ternel_tq1_linear_kernel, replayed against a measured sweep in
@@ -57,36 +65,55 @@ def select_kernel(layout: PackedTensorLayout, batch: int, dtype: torch.dtype) ->
     return _KERNEL_NAMES[code]
 
 
-def packed_matmul(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
-    """``x @ W.T`` for a packed ``W``, choosing the kernel by activation rows.
-
-    Leading dimensions of ``x`` are kept (src/ternel_mlx/modules.py:425-457).
-    """
+def matmul_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout) -> torch.Tensor:
+    """``x @ W.T`` for packed words ``W``, choosing the kernel by activation rows
+    and keeping the leading dimensions of ``x``."""
     if x.shape[-1] != layout.columns:
         raise FormatError(f"activation has {x.shape[-1]} columns, weight expects {layout.columns}")
     flat = x.reshape(-1, layout.columns)
     if select_kernel(layout, flat.shape[0], flat.dtype) == "gemm":
-        out = tq1_gemm(packed, flat, layout=layout, config=GemmConfig())
+        out = tq1_gemm_words(packed, flat, layout=layout, config=GemmConfig())
     else:
-        out = tq1_matmul(packed, flat, layout=layout, config=MatmulConfig())
+        out = tq1_matmul_words(packed, flat, layout=layout, config=MatmulConfig())
     return out.reshape(*x.shape[:-1], layout.rows)
 
 
+def packed_matmul(codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, *,
+                  layout: PackedTensorLayout) -> torch.Tensor:
+    """``x @ W.T`` for a packed ``W`` given as the reference's tiled pair,
+    choosing the kernel by activation rows (src/ternel_mlx/modules.py:425-457).
+    The pair is converted to packed words once and cached while it lives
+    unchanged (``kernels.words_of``)."""
+    if x.shape[-1] != layout.columns:
+        raise FormatError(f"activation has {x.shape[-1]} columns, weight expects {layout.columns}")
+    packed, pair_layout = words_of(codes, scales, groups_per_row=layout.groups_per_row, tile=layout.tile)
+    if (pair_layout.rows, pair_layout.columns) != (layout.rows, layout.columns):
+        raise FormatError(f"codes/scales hold a {pair_layout.rows}x{pair_layout.columns} tensor, "
+                          f"the layout {layout.rows}x{layout.columns}")
+    return matmul_words(packed, x, layout=layout)
+
+
 class _PackedWeight(nn.Module):
-    """Shared storage and loading of one packed weight."""
+    """Storage and loading of one packed weight: the packed words in device
+    memory, the reference's ``codes``/``scales`` as the state."""
 
     def __init__(self, layout: PackedTensorLayout, device=None) -> None:
         super().__init__()
         self.layout = layout
         if device is None and torch.cuda.is_available():
             device = torch.device("cuda", torch.cuda.current_device())
-        self.register_buffer("packed", torch.zeros(packed_shape(layout), dtype=torch.int32, device=device))
+        # The words are derived state: the state dict holds codes and scales.
+        self.register_buffer("packed", torch.zeros(packed_shape(layout), dtype=torch.int32, device=device),
+                             persistent=False)
+        self._tiled_key = None
+        self._tiled = None
 
+    # -- loading --------------------------------------------------------------
     def load_blocks(self, blocks, *, validate: bool = True) -> None:
         """Load canonical blocks (any shape holding ``rows * G`` 28-byte blocks).
 
         Every byte is scanned on the GPU first (fail-closed), then the blocks are
-        permuted into the packed layout.
+        permuted into the packed words.
         """
         tensor = as_device_blocks(blocks)
         if tensor.shape[0] != self.layout.groups:
@@ -99,12 +126,12 @@ class _PackedWeight(nn.Module):
         self.packed = pack_weights(tensor, layout=self.layout)
 
     def load_packed(self, codes, scales, *, validate: bool = True) -> None:
-        """Load the reference's tiled ``codes`` (u8) / ``scales`` (<u2) arrays."""
-        codes_np = codes.cpu().numpy() if isinstance(codes, torch.Tensor) else np.asarray(codes)
-        scales_np = scales.cpu().numpy() if isinstance(scales, torch.Tensor) else np.asarray(scales)
-        if scales_np.dtype == np.int16:
-            scales_np = scales_np.view("<u2")
-        self.load_blocks(unpack_blocks(codes_np, scales_np, layout=self.layout), validate=validate)
+        """Load the reference's tiled ``codes`` (u8) / ``scales`` (<u2) arrays:
+        device tensors are converted on the GPU, host arrays uploaded first."""
+        device = self.packed.device if self.packed.is_cuda else torch.device("cuda", torch.cuda.current_device())
+        codes_t = _as_device(codes, torch.uint8, device)
+        scales_t = _as_device(scales, torch.uint16, device)
+        self.packed = words_from_tiled(codes_t, scales_t, layout=self.layout, validate=validate)
 
     def load_weights(self, weights, strict: bool = True) -> "_PackedWeight":
         """MLX-style ``load_weights([("codes", c), ("scales", s)])`` (tests/test_mlx_modules.py:132-133)."""
@@ -141,20 +168,77 @@ class _PackedWeight(nn.Module):
                               f"{self.layout.rows}x{self.layout.columns}")
         self.packed = packed
 
+    # -- the reference's state ------------------------------------------------
+    def _tiled_pair(self) -> tuple[torch.Tensor, torch.Tensor]:
+        key = (self.packed.data_ptr(), self.packed._version)
+        if self._tiled_key != key:
+            self._tiled = tiled_from_words(self.packed, layout=self.layout)
+            self._tiled_key = key
+        return self._tiled
+
     @property
     def blocks(self) -> torch.Tensor:
-        """Canonical ``(rows, G, 28)`` blocks, by exact inverse permutation of ``packed``."""
+        """Canonical ``(rows, G, 28)`` device blocks, by exact inverse permutation."""
         return unpack_weights(self.packed, layout=self.layout)
 
     @property
-    def codes(self) -> np.ndarray:
-        """The reference's tiled code array, by exact permutation of the blocks."""
-        return pack_blocks(self.blocks.cpu().numpy(), layout=self.layout)[0]
+    def codes(self) -> torch.Tensor:
+        """The reference's tiled code array (uint8, device), by exact permutation."""
+        return self._tiled_pair()[0]
+
+    @codes.setter
+    def codes(self, value) -> None:
+        self.load_packed(value, self.scales)
 
     @property
-    def scales(self) -> np.ndarray:
-        """The reference's tiled scale array (raw fp16 bits as <u2)."""
-        return pack_blocks(self.blocks.cpu().numpy(), layout=self.layout)[1]
+    def scales(self) -> torch.Tensor:
+        """The reference's tiled scale array (uint16 raw fp16 bits, device)."""
+        return self._tiled_pair()[1]
+
+    @scales.setter
+    def scales(self, value) -> None:
+        self.load_packed(self.codes, value)
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars) -> None:
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        codes, scales = self._tiled_pair()
+        destination[prefix + "codes"] = codes if keep_vars else codes.detach()
+        destination[prefix + "scales"] = scales if keep_vars else scales.detach()
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs) -> None:
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                                      error_msgs)
+        keys = (prefix + "codes", prefix + "scales")
+        # Not registered parameters or buffers: the base class counts them as unexpected.
+        for k in keys:
+            if k in unexpected_keys:
+                unexpected_keys.remove(k)
+        present = [k in state_dict for k in keys]
+        if all(present):
+            try:
+                self.load_packed(state_dict[keys[0]], state_dict[keys[1]])
+            except FormatError as exc:
+                error_msgs.append(f"{prefix}codes/scales: {exc}")
+        else:
+            missing_keys.extend(k for k, p in zip(keys, present) if not p)
+
+
+def _as_device(array, dtype: torch.dtype, device) -> torch.Tensor:
+    if isinstance(array, torch.Tensor):
+        tensor = array
+        if dtype == torch.uint16 and tensor.dtype == torch.int16:
+            tensor = tensor.view(torch.uint16)
+    else:
+        host = np.ascontiguousarray(array)
+        if dtype == torch.uint16:
+            host = host.view("<u2") if host.dtype.itemsize == 2 else host.astype("<u2")
+            tensor = torch.from_numpy(host.view(np.int16)).view(torch.uint16)
+        else:
+            tensor = torch.from_numpy(host)
+    if tensor.dtype != dtype:
+        raise FormatError(f"expected {dtype}, got {tensor.dtype}")
+    return tensor.to(device).contiguous()
 
 
 class PackedLinear(_PackedWeight):
@@ -192,15 +276,22 @@ class PackedLinear(_PackedWeight):
                 f"{self.layout.bits_per_weight:.3f} bits/weight")
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return packed_matmul(self.packed, x, layout=self.layout)
+        return matmul_words(self.packed, x, layout=self.layout)
 
 
 class PackedEmbedding(_PackedWeight):
     """Token embedding decoded one row at a time (src/ternel_mlx/modules.py:498-549)."""
 
-    def __init__(self, layout: PackedTensorLayout, *, dtype: torch.dtype, device=None) -> None:
+    def __init__(self, layout: PackedTensorLayout, *, dtype: torch.dtype, device=None,
+                 canonical_rows: bool = False) -> None:
         super().__init__(layout, device=device)
         self.dtype = dtype
+        # Opt-in second copy of the table as canonical row-major blocks, which
+        # a gather reads contiguously (an 8192-token prefill gather ~2.6x
+        # faster) at the cost of the table's size again in device memory
+        # (170 MB at 151,936 x 5120). Off by default: one copy, as the
+        # reference keeps.
+        self.canonical_rows = canonical_rows
 
     @classmethod
     def from_embedding(cls, embedding: nn.Embedding, *, dtype: torch.dtype) -> "PackedEmbedding":
@@ -229,20 +320,20 @@ class PackedEmbedding(_PackedWeight):
         return f"{self.layout.rows} x {self.layout.columns}, tile={self.layout.tile}, {self.dtype}"
 
     def forward(self, indices: torch.Tensor) -> torch.Tensor:
-        """Rows for ``indices`` of any shape; ids outside the table read as zeros.
-
-        Gathers read a canonical row-major copy of the table (``row_blocks``): in the
-        packed layout a row's words lie in separate 256-byte segments, so a gather
-        would fetch whole segments for 4 bytes each."""
+        """Rows for ``indices`` of any shape and integer dtype; ids outside the
+        table read as zeros (src/ternel_mlx/modules.py:527-545)."""
         flat = indices.reshape(-1)
-        rows = tq1_get_rows_canonical(self.row_blocks(), flat, layout=self.layout, dtype=self.dtype)
+        if self.canonical_rows:
+            rows = tq1_get_rows_canonical(self.row_blocks(), flat, layout=self.layout, dtype=self.dtype)
+        else:
+            rows = tq1_get_rows_words(self.packed, flat, layout=self.layout, dtype=self.dtype)
         return rows.reshape(*indices.shape, self.layout.columns)
 
     def row_blocks(self) -> torch.Tensor:
-        """The table as canonical ``(rows, G, 28)`` device blocks, derived from the packed
-        words on first use and again whenever they are replaced or written (28 bytes per
-        128 weights: 170 MB for a 151,936 x 5120 table). Not part of the state dict. Call it
-        once before capturing a graph that gathers, so the capture holds no rebuild."""
+        """The table as canonical ``(rows, G, 28)`` device blocks (``canonical_rows``),
+        derived from the packed words on first use and again whenever they are
+        replaced or written. Not part of the state dict. Call it once before
+        capturing a graph that gathers, so the capture holds no rebuild."""
         key = (self.packed.data_ptr(), self.packed._version, self.packed.device)
         if getattr(self, "_row_blocks_key", None) != key:
             self._row_blocks = unpack_weights(self.packed, layout=self.layout)
@@ -251,7 +342,7 @@ class PackedEmbedding(_PackedWeight):
 
     def as_linear(self, x: torch.Tensor) -> torch.Tensor:
         """Tied output head: the embedding table used as a matmul."""
-        return packed_matmul(self.packed, x, layout=self.layout)
+        return matmul_words(self.packed, x, layout=self.layout)
 
 
 class PackedSwiGLU(nn.Module):
@@ -312,7 +403,7 @@ class PackedSwiGLU(nn.Module):
         if x.shape[-1] != self.layout.columns:
             raise FormatError(f"activations have {x.shape[-1]} columns, expected {self.layout.columns}")
         flat = x.reshape(-1, self.layout.columns)
-        return tq1_swiglu(self.packed, flat, layout=self.layout).reshape(*x.shape[:-1], self.hidden)
+        return tq1_swiglu_words(self.packed, flat, layout=self.layout).reshape(*x.shape[:-1], self.hidden)
 
 
 def replace_with_packed(model: nn.Module, *, embedding_dtype: torch.dtype = torch.float16) -> nn.Module:
@@ -361,6 +452,7 @@ __all__ = [
     "PackedLinear",
     "PackedSwiGLU",
     "load_packed_model",
+    "matmul_words",
     "packed_matmul",
     "replace_with_packed",
     "select_kernel",

@@ -14,7 +14,7 @@ from tests.gpu_util import layout, pack, random_blocks, to_dev
 from ternel_amd.artifact import load_safetensors_tensor, load_sidecar_tensor, read_sidecar, save_safetensors, \
     sidecar_tensors, write_sidecar
 from ternel_amd.format import FormatError
-from ternel_amd.kernels import tq1_matmul
+from ternel_amd.kernels import tq1_matmul_words
 from ternel_amd.modules import PackedEmbedding, PackedLinear, load_packed_model, replace_with_packed
 
 pytestmark = pytest.mark.gpu
@@ -29,8 +29,8 @@ def test_sidecar_tensor_loads_to_the_same_packed_words(tmp_path, rows: int, colu
     assert (lay.rows, lay.columns) == (rows, columns)
     assert torch.equal(packed, pack(blocks))
     x = np.random.default_rng(rows).normal(0, 1, size=(1, columns)).astype(np.float32)
-    got = tq1_matmul(packed, to_dev(x), layout=lay).cpu().numpy()
-    np.testing.assert_array_equal(got, tq1_matmul(pack(blocks), to_dev(x), layout=layout(rows, columns)).cpu().numpy())
+    got = tq1_matmul_words(packed, to_dev(x), layout=lay).cpu().numpy()
+    np.testing.assert_array_equal(got, tq1_matmul_words(pack(blocks), to_dev(x), layout=layout(rows, columns)).cpu().numpy())
     oracle = O.oracle_matmul(blocks, x, rows=rows, columns=columns)
     assert O.compare(got, oracle)["normalised_max_abs_error"] < 1e-3
 

@@ -17,7 +17,7 @@ import torch
 from oracle import tq1_oracle as O
 from tests.gpu_util import layout, pack, random_blocks, to_dev
 from ternel_amd.format import FormatError
-from ternel_amd.kernels import GemmConfig, tq1_gemm
+from ternel_amd.kernels import GemmConfig, tq1_gemm_words
 
 pytestmark = pytest.mark.gpu
 
@@ -30,7 +30,7 @@ FORMS = ("tile", "direct", "wide")
 
 def run(blocks: np.ndarray, x16: np.ndarray, *, k_split: int = 0, form: str = "auto") -> np.ndarray:
     rows, g, _ = blocks.shape
-    out = tq1_gemm(pack(blocks), to_dev(x16), layout=layout(rows, g * 128),
+    out = tq1_gemm_words(pack(blocks), to_dev(x16), layout=layout(rows, g * 128),
                    config=GemmConfig(k_split=k_split, form=form))
     torch.cuda.synchronize()
     return out.float().cpu().numpy().astype(np.float64)
@@ -136,18 +136,16 @@ def test_gemm_propagates_non_finite_activations(form: str) -> None:
 def test_gemm_rejects_other_dtypes_and_bad_splits() -> None:
     blocks = pack(random_blocks(256, 384, seed=1))
     lay = layout(256, 384)
-    with pytest.raises(FormatError, match="float16"):
-        tq1_gemm(blocks, torch.zeros((4, 384), device="cuda"), layout=lay)
     with pytest.raises(FormatError, match="does not divide the tensor's 3 groups"):
-        tq1_gemm(blocks, torch.zeros((4, 384), device="cuda", dtype=torch.float16), layout=lay,
+        tq1_gemm_words(blocks, torch.zeros((4, 384), device="cuda", dtype=torch.float16), layout=lay,
                  config=GemmConfig(k_split=2))
     with pytest.raises(FormatError, match="activations have 256 columns, expected 384"):
-        tq1_gemm(blocks, torch.zeros((4, 256), device="cuda", dtype=torch.float16), layout=lay)
+        tq1_gemm_words(blocks, torch.zeros((4, 256), device="cuda", dtype=torch.float16), layout=lay)
     with pytest.raises(FormatError, match="at most 64 activation rows"):
-        tq1_gemm(blocks, torch.zeros((65, 384), device="cuda", dtype=torch.float16), layout=lay,
+        tq1_gemm_words(blocks, torch.zeros((65, 384), device="cuda", dtype=torch.float16), layout=lay,
                  config=GemmConfig(form="direct"))
     with pytest.raises(FormatError, match="stream-K"):
-        tq1_gemm(blocks, torch.zeros((4, 384), device="cuda", dtype=torch.float16), layout=lay,
+        tq1_gemm_words(blocks, torch.zeros((4, 384), device="cuda", dtype=torch.float16), layout=lay,
                  config=GemmConfig(form="wide", k_split=3))
 
 

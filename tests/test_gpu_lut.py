@@ -15,7 +15,7 @@ import torch
 from oracle import tq1_oracle as O
 from tests.gpu_util import layout, pack, positional_all_slots, positional_tail, random_blocks, to_dev
 from ternel_amd.format import FormatError
-from ternel_amd.kernels import MatmulConfig, tq1_matmul
+from ternel_amd.kernels import MatmulConfig, tq1_matmul_words
 
 pytestmark = pytest.mark.gpu
 
@@ -27,7 +27,7 @@ def run(blocks: np.ndarray, x: np.ndarray, *, batch_tile: int = 1, k_split: int 
         dtype=torch.float32) -> np.ndarray:
     rows, g, _ = blocks.shape
     lay = layout(rows, g * 128)
-    out = tq1_matmul(pack(blocks), to_dev(x).to(dtype), layout=lay,
+    out = tq1_matmul_words(pack(blocks), to_dev(x).to(dtype), layout=lay,
                      config=MatmulConfig(batch_tile=batch_tile, k_split=k_split))
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
@@ -87,7 +87,7 @@ def test_activation_dtypes_round_once_at_the_store(dtype) -> None:
     raw = torch.from_numpy(rng.normal(0.0, 1.0, size=(3, 384)).astype(np.float32)).to(dtype)
     x = raw.float().numpy()
     lay = layout(256, 384)
-    out = tq1_matmul(pack(blocks), raw.to("cuda"), layout=lay, config=MatmulConfig(batch_tile=1, k_split=1))
+    out = tq1_matmul_words(pack(blocks), raw.to("cuda"), layout=lay, config=MatmulConfig(batch_tile=1, k_split=1))
     assert out.dtype == dtype
     want = O.lut23_matmul(blocks, x, rows=256, columns=384)
     # Only the final store is narrowed: the result is the fp32 answer rounded once.
@@ -168,13 +168,13 @@ def test_activation_checks_match_the_reference_messages() -> None:
     blocks = pack(random_blocks(256, 384, seed=1))
     lay = layout(256, 384)
     with pytest.raises(FormatError, match="activations have 256 columns, expected 384"):
-        tq1_matmul(blocks, torch.zeros((1, 256), device="cuda"), layout=lay)
+        tq1_matmul_words(blocks, torch.zeros((1, 256), device="cuda"), layout=lay)
     with pytest.raises(FormatError, match="2-D"):
-        tq1_matmul(blocks, torch.zeros((384,), device="cuda"), layout=lay)
+        tq1_matmul_words(blocks, torch.zeros((384,), device="cuda"), layout=lay)
     with pytest.raises(FormatError, match="empty batch"):
-        tq1_matmul(blocks, torch.zeros((0, 384), device="cuda"), layout=lay)
+        tq1_matmul_words(blocks, torch.zeros((0, 384), device="cuda"), layout=lay)
     with pytest.raises(FormatError, match="activations must be one of"):
-        tq1_matmul(blocks, torch.zeros((1, 384), device="cuda", dtype=torch.float64), layout=lay)
+        tq1_matmul_words(blocks, torch.zeros((1, 384), device="cuda", dtype=torch.float64), layout=lay)
 
 
 @pytest.mark.parametrize("batch", (1, 2, 5, 16))
@@ -182,7 +182,7 @@ def test_auto_configuration_meets_the_north_star_tolerance(batch: int) -> None:
     rows, columns = 2048, 5120
     blocks = random_blocks(rows, columns, seed=batch)
     x = np.random.default_rng(batch).normal(0, 1, size=(batch, columns)).astype(np.float16)
-    got = tq1_matmul(pack(blocks), to_dev(x), layout=layout(rows, columns)).float().cpu().numpy()
+    got = tq1_matmul_words(pack(blocks), to_dev(x), layout=layout(rows, columns)).float().cpu().numpy()
     oracle = O.oracle_matmul(blocks, x.astype(np.float32), rows=rows, columns=columns)
     result = O.compare(got, oracle)
     assert result["normalised_max_abs_error"] < NORTH_STAR_TOLERANCE
@@ -200,7 +200,7 @@ AUTO_SHAPES = ((128, 128), (64, 256), (300, 640), (8192, 1024), (2048, 5120), (1
 
 def run_auto(blocks: np.ndarray, x: np.ndarray, dtype=torch.float32) -> torch.Tensor:
     rows, g, _ = blocks.shape
-    out = tq1_matmul(pack(blocks), to_dev(x).to(dtype), layout=layout(rows, g * 128), config=MatmulConfig())
+    out = tq1_matmul_words(pack(blocks), to_dev(x).to(dtype), layout=layout(rows, g * 128), config=MatmulConfig())
     torch.cuda.synchronize()
     return out
 

@@ -1,5 +1,5 @@
 """Embedding gather and the module API (PackedLinear / PackedEmbedding /
-packed_matmul) on the GPU, against the oracle."""
+matmul_words) on the GPU, against the oracle."""
 
 from __future__ import annotations
 
@@ -12,9 +12,9 @@ from oracle import tq1_oracle as O
 from tests.gpu_util import layout, pack, random_blocks, to_dev
 from ternel_amd.format import FormatError
 from ternel_amd import _lib
-from ternel_amd.kernels import tq1_get_rows, tq1_get_rows_canonical
+from ternel_amd.kernels import tq1_get_rows_words, tq1_get_rows_canonical
 from ternel_amd.layout import pack_blocks
-from ternel_amd.modules import PackedEmbedding, PackedLinear, packed_matmul, replace_with_packed, select_kernel
+from ternel_amd.modules import PackedEmbedding, PackedLinear, matmul_words, replace_with_packed, select_kernel
 
 pytestmark = pytest.mark.gpu
 
@@ -25,7 +25,7 @@ def test_get_rows_is_bit_exact(rows: int, columns: int, dtype) -> None:
     blocks = random_blocks(rows, columns, seed=rows + 3)
     rng = np.random.default_rng(rows)
     ids = np.unique(np.concatenate([[0, rows - 1, rows // 2], rng.integers(0, rows, size=16)])).astype(np.int64)
-    got = tq1_get_rows(pack(blocks), to_dev(ids), layout=layout(rows, columns), dtype=dtype)
+    got = tq1_get_rows_words(pack(blocks), to_dev(ids), layout=layout(rows, columns), dtype=dtype)
     want = O.get_rows_reference(blocks, ids, rows=rows, columns=columns,
                                 dtype=np.float32 if dtype == torch.float32 else np.float16)
     np.testing.assert_array_equal(got.cpu().numpy(), want)
@@ -34,7 +34,7 @@ def test_get_rows_is_bit_exact(rows: int, columns: int, dtype) -> None:
 def test_get_rows_bf16_rounds_the_exact_value_once() -> None:
     blocks = random_blocks(300, 256, seed=9)
     ids = np.arange(0, 300, 7, dtype=np.int64)
-    got = tq1_get_rows(pack(blocks), to_dev(ids), layout=layout(300, 256), dtype=torch.bfloat16)
+    got = tq1_get_rows_words(pack(blocks), to_dev(ids), layout=layout(300, 256), dtype=torch.bfloat16)
     want = O.get_rows_reference(blocks, ids, rows=300, columns=256, dtype=np.float32)
     np.testing.assert_array_equal(got.float().cpu().numpy(), torch.from_numpy(want).to(torch.bfloat16).float().numpy())
 
@@ -42,7 +42,7 @@ def test_get_rows_bf16_rounds_the_exact_value_once() -> None:
 def test_get_rows_repeats_and_out_of_range_ids() -> None:
     blocks = random_blocks(512, 256, seed=44)
     ids = torch.tensor([7, 7, 511, 0, 7, 512, 100000, -1], dtype=torch.int64, device="cuda")
-    got = tq1_get_rows(pack(blocks), ids, layout=layout(512, 256), dtype=torch.float32).cpu().numpy()
+    got = tq1_get_rows_words(pack(blocks), ids, layout=layout(512, 256), dtype=torch.float32).cpu().numpy()
     np.testing.assert_array_equal(got[0], got[1])
     np.testing.assert_array_equal(got[0], got[4])
     assert not got[5:].any()
@@ -61,7 +61,7 @@ def test_canonical_gather_is_bit_identical_to_the_packed_one(rows: int, columns:
     lay = layout(rows, columns)
     canonical = torch.from_numpy(blocks).cuda()
     got = tq1_get_rows_canonical(canonical, ids, layout=lay, dtype=dtype)
-    packed = tq1_get_rows(pack(blocks), ids, layout=lay, dtype=dtype)
+    packed = tq1_get_rows_words(pack(blocks), ids, layout=lay, dtype=dtype)
     assert torch.equal(got.view(torch.int16 if dtype != torch.float32 else torch.int32),
                        packed.view(torch.int16 if dtype != torch.float32 else torch.int32))
     assert not got[4:6].any()
@@ -80,7 +80,7 @@ def test_gather_into_an_unaligned_output(entry: str) -> None:
     lay = layout(rows, columns)
     table = pack(blocks) if entry == "packed" else torch.from_numpy(blocks).cuda()
     ids = torch.tensor([5, 299, 0, 150], dtype=torch.int64, device="cuda")
-    aligned = (tq1_get_rows if entry == "packed" else tq1_get_rows_canonical)(table, ids, layout=lay,
+    aligned = (tq1_get_rows_words if entry == "packed" else tq1_get_rows_canonical)(table, ids, layout=lay,
                                                                               dtype=torch.float16)
     buf = torch.zeros(ids.numel() * columns + 1, dtype=torch.float16, device="cuda")
     fn = _lib.lib().ternel_tq1_get_rows if entry == "packed" else _lib.lib().ternel_tq1_get_rows_canonical
@@ -102,10 +102,10 @@ def test_canonical_gather_rejects_a_wrong_table() -> None:
 def test_get_rows_rejects_bad_indices() -> None:
     blocks = pack(random_blocks(256, 256, seed=1))
     with pytest.raises(FormatError, match="1-D"):
-        tq1_get_rows(blocks, torch.zeros((2, 2), dtype=torch.int64, device="cuda"), layout=layout(256, 256),
+        tq1_get_rows_words(blocks, torch.zeros((2, 2), dtype=torch.int64, device="cuda"), layout=layout(256, 256),
                      dtype=torch.float32)
     with pytest.raises(FormatError, match="empty"):
-        tq1_get_rows(blocks, torch.zeros((0,), dtype=torch.int64, device="cuda"), layout=layout(256, 256),
+        tq1_get_rows_words(blocks, torch.zeros((0,), dtype=torch.int64, device="cuda"), layout=layout(256, 256),
                      dtype=torch.float32)
 
 
@@ -122,8 +122,8 @@ def test_packed_linear_loads_the_reference_tiled_arrays() -> None:
     module, blocks = loaded_linear(512, 640, seed=77)
     np.testing.assert_array_equal(module.blocks.cpu().numpy(), blocks)
     codes, scales = pack_blocks(blocks, layout=module.layout)
-    np.testing.assert_array_equal(module.codes, codes)
-    np.testing.assert_array_equal(module.scales, scales)
+    np.testing.assert_array_equal(module.codes.cpu().numpy(), codes)
+    np.testing.assert_array_equal(module.scales.cpu().numpy(), scales)
 
 
 @pytest.mark.parametrize("batch", (1, 3, 16, 200))
@@ -215,5 +215,5 @@ def test_replace_with_packed_swaps_every_linear_and_embedding() -> None:
 def test_packed_matmul_function_matches_the_module() -> None:
     module, blocks = loaded_linear(256, 384, seed=12)
     x = torch.randn(3, 384, device="cuda", dtype=torch.float16)
-    np.testing.assert_array_equal(packed_matmul(module.packed, x, layout=module.layout).cpu().numpy(),
+    np.testing.assert_array_equal(matmul_words(module.packed, x, layout=module.layout).cpu().numpy(),
                                   module(x).cpu().numpy())

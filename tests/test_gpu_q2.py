@@ -9,7 +9,7 @@ import torch
 from oracle import tq1_oracle as O
 from tests.gpu_util import layout, pack, to_dev
 from ternel_amd.format import FormatError, convert_q2_blocks
-from ternel_amd.kernels import tq1_matmul
+from ternel_amd.kernels import tq1_matmul_words
 
 pytestmark = pytest.mark.gpu
 
@@ -74,6 +74,6 @@ def test_device_input_stays_on_the_device_and_products_agree() -> None:
     assert out.is_cuda and out.shape == (rows * columns // 128, 28)
     blocks = out.cpu().numpy().reshape(rows, columns // 128, 28)
     x = np.random.default_rng(9).normal(0, 1, size=(2, columns)).astype(np.float32)
-    got = tq1_matmul(pack(blocks), to_dev(x), layout=layout(rows, columns)).cpu().numpy()
+    got = tq1_matmul_words(pack(blocks), to_dev(x), layout=layout(rows, columns)).cpu().numpy()
     want = x.astype(np.float64) @ O.q2_dense_weights(source, rows=rows, columns=columns).T
     assert O.compare(got, want)["normalised_max_abs_error"] < 1e-5

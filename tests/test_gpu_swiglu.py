@@ -10,7 +10,7 @@ import torch
 from oracle import tq1_oracle as O
 from tests.gpu_util import layout, pack, random_blocks, to_dev
 from ternel_amd.format import FormatError
-from ternel_amd.kernels import tq1_swiglu
+from ternel_amd.kernels import tq1_swiglu_words
 from ternel_amd.layout import interleave_gate_up
 from ternel_amd.modules import PackedLinear, PackedSwiGLU
 
@@ -36,6 +36,14 @@ def fp16_spacing(v: torch.Tensor) -> torch.Tensor:
     return torch.ldexp(torch.ones_like(v), exponent - 11).clamp_min(2.0 ** -24)
 
 
+def spacing(v: torch.Tensor, dtype) -> torch.Tensor:
+    """Distance from |v| to the next value of ``dtype`` (fp16, bf16 or fp32)."""
+    if dtype == torch.float16:
+        return fp16_spacing(v)
+    bits = {torch.bfloat16: 8, torch.float32: 24}[dtype]
+    return torch.ldexp(torch.ones_like(v), torch.frexp(v).exponent - bits).clamp_min(2.0 ** -126)
+
+
 def oracle(gate_blocks, up_blocks, x: np.ndarray) -> np.ndarray:
     hidden, g, _ = gate_blocks.shape
     gv = O.oracle_matmul(gate_blocks, x, rows=hidden, columns=g * 128)
@@ -57,27 +65,27 @@ def test_fused_swiglu_matches_the_unfused_layers(dtype, batch: int, hidden: int,
     assert got.dtype == dtype and got.shape == (batch, hidden)
     want, gv, uv = unfused(gate_blocks, up_blocks, x, with_operands=True)
     diff = (got.float() - want.float()).abs()
-    if dtype == torch.float16 and batch > 4:
-        # The fp16 GEMM path tiles a 2 x hidden weight differently from a
-        # hidden one, so its fp32 sums differ by up to the accumulation bound
-        # (columns x eps x |x||W|, per operand) and may then round to another
-        # fp16 value (a step of either neighbouring binade); z moves by at most
-        # that through its partial derivatives, plus one step of its own
-        # rounding.
+    if (dtype == torch.float16 and batch > 4) or batch == 1:
+        # The fp16 GEMM path, and at one vector the stream GEMV, split a
+        # 2 x hidden weight differently from a hidden one, so the fp32 sums
+        # differ by up to the accumulation bound (columns x eps x |x||W|, per
+        # operand) and may then round to another value of the activation type
+        # (a step of either neighbouring binade); z moves by at most that
+        # through its partial derivatives, plus one step of its own rounding.
         xa = np.abs(x.float().cpu().numpy().astype(np.float64))
         eps = float(np.finfo(np.float32).eps)
         accumulation = [torch.from_numpy(columns * eps * (xa @ np.abs(O.dense_weights(b, rows=hidden,
                                                                                       columns=columns)).T)).cuda()
                         for b in (gate_blocks, up_blocks)]
-        dg = 2 * accumulation[0] + 2 * fp16_spacing(gv)
-        du = 2 * accumulation[1] + 2 * fp16_spacing(uv)
+        dg = 2 * accumulation[0] + 2 * spacing(gv, dtype)
+        du = 2 * accumulation[1] + 2 * spacing(uv, dtype)
         sig = torch.sigmoid(gv)
         dz_dg = (uv * sig * (1.0 + gv * (1.0 - sig))).abs()
         dz_du = (gv * sig).abs()
-        bound = 1.01 * (dz_dg * dg + dz_du * du) + fp16_spacing(want.float())
+        bound = 1.01 * (dz_dg * dg + dz_du * du) + spacing(want.float(), dtype)
         assert bool((diff <= bound).all()), float((diff - bound).max())
     else:
-        # The LUT path (batches up to 4, every bf16/fp32 batch) sums each row
+        # The LUT path (batches of 2 to 4, every bf16/fp32 batch) sums each row
         # in the same chunk order for the fused and the separate weights: gate
         # and up round to the same values and z agrees to SiLU's exp (an fp32
         # ulp against torch's) and one rounding step of z.
@@ -106,7 +114,7 @@ def test_the_fused_weight_is_the_interleaved_gate_and_up() -> None:
 def test_an_odd_row_count_is_rejected() -> None:
     blocks = random_blocks(255, 256, seed=3)
     with pytest.raises(FormatError, match="rows must be even"):
-        tq1_swiglu(pack(blocks), torch.zeros((1, 256), device="cuda", dtype=torch.float16), layout=layout(255, 256))
+        tq1_swiglu_words(pack(blocks), torch.zeros((1, 256), device="cuda", dtype=torch.float16), layout=layout(255, 256))
 
 
 def test_non_finite_gate_values_follow_ieee() -> None:
