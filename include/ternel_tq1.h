@@ -35,17 +35,15 @@
  * the LUT path), fp32 accumulation throughout.
  *
  * Workspaces: a split workspace starts with a fixed 64 KiB region of
- * arrival counters whose last 32-bit word is the workspace's error word, then
- * a fixed 32 MiB region of the LUT23 kernel's published pieces (64-bit
- * {value, flag} slots), then the fp32 partials of the other split kernels. The
- * first two regions must be zero the first time the workspace is used; every
- * successful call leaves them zero again, so one zero-filled workspace can
- * serve calls of any shape (the reference's stream-K contract,
- * cuda/tq1_lut23_streamk.cu:320-334). Calls sharing one workspace must not
- * overlap in time (one workspace per stream). A kernel whose bounded wait for
- * another workgroup's published partial gives up sets the error word
- * (ternel_tq1_workspace_error) and may leave counters or slots set: zero the
- * workspace again before reusing it.
+ * arrival counters whose last 32-bit word is the workspace's error word,
+ * followed by fp32 partials. The counter region must be zero the first time
+ * the workspace is used; every successful call leaves it zero again, so one
+ * zero-filled workspace can serve calls of any shape (the reference's
+ * stream-K contract, cuda/tq1_lut23_streamk.cu:320-334). Calls sharing one
+ * workspace must not overlap in time (one workspace per stream). A kernel
+ * whose bounded wait for another workgroup's published partial gives up sets
+ * the error word (ternel_tq1_workspace_error) and may leave counters set: zero
+ * the workspace again before reusing it.
  */
 #ifndef TERNEL_TQ1_H
 #define TERNEL_TQ1_H
@@ -148,8 +146,8 @@ int ternel_tq1_tiled_from_words(const uint32_t *packed, int64_t rows, int64_t co
  * A split is reduced inside the same launch, in chunk order (deterministic).
  * ws: at least ternel_tq1_matmul_workspace_bytes(...) bytes (0 when the split
  * resolves to 1; ws may then be NULL); see the workspace contract above.
- * A split batch whose (row block, batch tile) counters or pieces exceed their
- * regions runs as several launches of as many rows as they hold, in order.
+ * A split batch whose (row block, batch tile) counters exceed the counter
+ * region runs as several launches of as many rows as it holds, in order.
  */
 int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
                       int64_t columns, int dtype, int batch_tile, int k_split, void *ws, size_t ws_bytes,
@@ -249,8 +247,8 @@ size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t column
 /*
  * Reads a workspace's error word (synchronises `stream`): *error = 0, or a
  * bitmask of the kernels whose bounded wait for a published partial gave up
- * (1 = the LUT23 kernel's split-K fix-up, 2 = the wide GEMM's stream-K
- * reduction). No
+ * (2 = the wide GEMM's stream-K reduction; the LUT23 and direct-form
+ * fix-ups never wait). No
  * counterpart in the reference, whose fix-ups (cuda/tq1_lut23_streamk.cu:
  * 194-256) spin without a bound; here a wait that cannot complete is reported
  * instead of hanging the device or summing unpublished data.

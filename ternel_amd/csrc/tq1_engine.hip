@@ -642,38 +642,27 @@ __device__ __forceinline__ void split_word(uint32_t word, uint32_t base, uint32_
     split_pair(__builtin_amdgcn_perm(0u, word, 0x0c030c01u), base, lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
 }
 
-// Adds the k published pieces of one output (stride apart) left to right.
-// Each is a 64-bit slot {fp32 value, flag 1}, written by one atomic store: the
-// count of arrivals says every piece has been stored, the flag that its store
-// is visible here. All loads of a batch of up to 32 are in flight at once (one
-// memory round trip per batch); a slot whose flag is not visible yet is polled
-// (at most spin_limit times -- a negative limit gives up at once, the tests'
-// way in), and every slot is cleared for the next call.
-__device__ __forceinline__ float sum_pieces_in_order(uint64_t *src, int64_t stride, int k, int spin_limit,
-                                                     bool &failed) {
+// Adds partial[0..k) (stride apart) left to right. The agent-coherent loads of
+// up to 32 chunks are all issued before the first add, so a split costs one
+// memory round trip here rather than one per chunk.
+__device__ __forceinline__ float sum_partials_in_order(const float *src, int64_t stride, int k) {
     constexpr int kBatch = 32;
-    if (spin_limit < 0) failed = true;
     float a = 0.0f;
     for (int z0 = 0; z0 < k; z0 += kBatch) {
-        uint64_t v[kBatch];
+        float v[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
             v[u] = z0 + u < k ? __hip_atomic_load(src + (z0 + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : 0;
+                              : 0.0f;
+        if (z0 == 0) {
+            a = v[0];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            if (z0 + u >= k) continue;
-            for (int spin = 0; (v[u] >> 32) == 0 && !failed; ++spin) {
-                if (spin >= spin_limit) {
-                    failed = true;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-                v[u] = __hip_atomic_load(src + (z0 + u) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            const float f = __uint_as_float(static_cast<uint32_t>(v[u]));
-            a = z0 + u == 0 ? f : a + f;
-            __hip_atomic_store(src + (z0 + u) * stride, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int u = 1; u < kBatch; ++u)
+                if (u < k) a += v[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (z0 + u < k) a += v[u];
         }
     }
     return a;
@@ -694,8 +683,8 @@ __device__ __forceinline__ T swiglu_pair(T gate, T up) {
 template <typename T, int C, int BT, bool GLU = false, int KW = 1>
 __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     const uint32_t *__restrict__ packed, const T *__restrict__ x, T *__restrict__ y,
-    uint64_t *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
-    int k_split, int spin_limit) {
+    float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
+    int k_split) {
     // KW waves share each 64-row tile: wave stream s sums blocks
     // [s * CB, (s + 1) * CB) of every sub-chunk, so all of a sub-chunk's words
     // can be in flight from the start without one wave stalling on their issue.
@@ -858,23 +847,28 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         for (int j = 0; j < BT; ++j) store(j, acc[j]);
         return;
     }
-    // Split: publish the partial as {value, flag} with one 64-bit agent-scope
-    // store per output, then count this chunk in. The workgroup that brings
-    // the count to k_split adds the chunks in chunk order, waiting on each
-    // slot's flag -- which is what makes the hand-off correct with relaxed
-    // atomics only (no cache writeback or invalidate). Waiting for the stores
-    // to be acknowledged before counting is for speed alone: the last arriver
-    // then finds every flag on its first load (without it, measured on MI355X,
-    // its fix-up took a second round trip: gate/up 9.5 -> 10.7 us).
+    // Split: publish the partial with agent-scope atomic stores (sc1: written
+    // through to the device's coherence point, past the per-XCD L2), wait until
+    // every one is acknowledged there (vmcnt(0)), then count this chunk in with
+    // a relaxed agent-scope atomic. The workgroup that brings the count to
+    // k_split reads the chunks with agent-scope atomic loads (sc1: from the
+    // coherence point) and adds them in chunk order. This is the instruction
+    // sequence of an agent-scope release/acquire hand-off on gfx950 without
+    // the L2 writeback and invalidate, which concern only data written without
+    // sc1 -- and this hand-off writes none. The compiler barriers keep the
+    // count from moving above the wait. (A {value, flag} slot protocol that
+    // needs no acknowledgement measured 9.6 -> 10.9 us for gate/up on
+    // MI355X; a __threadfence version about 60 us.)
     if (row_ok) {
 #pragma unroll
         for (int j = 0; j < BT; ++j)
             if (b0 + j < M)
-                __hip_atomic_store(partial + (static_cast<int64_t>(blockIdx.z) * M + b0 + j) * N + row,
-                                   (uint64_t{1} << 32) | __float_as_uint(acc[j]), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(partial + (static_cast<int64_t>(blockIdx.z) * M + b0 + j) * N + row, acc[j],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    asm volatile("" ::: "memory");
     wait_vector_memory();
+    asm volatile("" ::: "memory");
     TQ1_PHASE(lut_wave_id, 4);  // partial stored and acknowledged
     __syncthreads();
     unsigned *counter = counters + static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
@@ -885,19 +879,18 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     TQ1_PHASE(lut_wave_id, 5);  // arrival counted
     if (!s_last) return;
     const int64_t stride = static_cast<int64_t>(M) * N;
-    bool failed = false;
 #pragma unroll
     for (int j = 0; j < BT; ++j) {
-        uint64_t *src = partial + static_cast<int64_t>(b0 + j) * N + row;
-        store(j, row_ok && b0 + j < M ? sum_pieces_in_order(src, stride, k_split, spin_limit, failed) : 0.0f);
+        const float *src = partial + static_cast<int64_t>(b0 + j) * N + row;
+        store(j, row_ok && b0 + j < M ? sum_partials_in_order(src, stride, k_split) : 0.0f);
     }
-    if (__builtin_amdgcn_ballot_w64(failed) && lane == 0)
-        __hip_atomic_fetch_or(counters + kWorkspaceErrorSlot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();  // every wave has read its slots before the counter is re-armed
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     TQ1_PHASE(lut_wave_id, 6);  // fix-up done
 }
 
+// The elementwise SwiGLU step over a linear's output whose rows alternate
+// gate, up: z[i] = SiLU(y[2i]) * y[2i+1] (N even, so pairs never straddle a
+// batch row).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void swiglu_pairs_kernel(const T *__restrict__ y, T *__restrict__ z,
                                                                 int64_t pairs) {
@@ -2068,12 +2061,8 @@ static_assert(kCounterRegionBytes == kWorkspaceCounterBytes, "one counter region
 constexpr int kErrorSlot = kCounterSlots - 1;
 static_assert(kErrorSlot == kWorkspaceErrorSlot, "one error word");
 constexpr int kUsableCounters = kCounterSlots - 16;
-// The LUT23 kernel's published pieces follow the counters in a region of
-// their own: each 64-bit slot holds a flag that must be zero between calls, so
-// no other kernel's partials may ever land there.
-constexpr size_t kLutRegionBytes = 32u << 20;
-// Partials of every other split kernel start here.
-constexpr size_t kPartialOffset = kCounterRegionBytes + kLutRegionBytes;
+// Partials of every split kernel start here.
+constexpr size_t kPartialOffset = kCounterRegionBytes;
 
 struct LutPlan {
     int batch_tile;
@@ -2170,33 +2159,15 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
         plan->batch_tiles = 65535;
         plan->launch_vectors = std::min<int64_t>(plan->launch_vectors, 65535 * static_cast<int64_t>(plan->batch_tile));
     }
-    if (plan->k_split > 1) {
-        // The pieces of one launch must fit the LUT region: fewer vectors per
-        // launch, or -- when not even one batch tile fits -- no split.
-        const int64_t per_vector = static_cast<int64_t>(plan->k_split) * rows * sizeof(uint64_t);
-        int64_t fit = static_cast<int64_t>(kLutRegionBytes) / per_vector;
-        fit -= fit % plan->batch_tile;
-        if (fit < plan->batch_tile) {
-            if (k_split > 1)
-                return fail(TERNEL_TQ1_EINVAL, "k split %d of %lld rows needs more split-K workspace than the %zu-byte "
-                            "region holds", k_split, static_cast<long long>(rows), kLutRegionBytes);
-            plan->k_split = 1;
-            plan->chunk_groups = static_cast<int>(G);
-            while (plan->chunk_groups % plan->chunk) plan->chunk /= 2;
-        } else if (plan->launch_vectors > fit) {
-            plan->launch_vectors = fit;
-            plan->batch_tiles = fit / plan->batch_tile;
-        }
-    }
     plan->counter_bytes = plan->k_split > 1 ? kCounterRegionBytes : 0;
     plan->partial_bytes = plan->k_split > 1 ? static_cast<size_t>(plan->k_split) *
-                                                  static_cast<size_t>(plan->launch_vectors) * rows * sizeof(uint64_t)
+                                                  static_cast<size_t>(plan->launch_vectors) * rows * sizeof(float)
                                             : 0;
     return TERNEL_TQ1_OK;
 }
 
 template <typename T, int C, int BT, bool GLU = false>
-void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *x, void *y, uint64_t *partial,
+void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *x, void *y, float *partial,
                        unsigned *counters, int64_t M, int64_t rows, int G, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.batch_tiles),
                     static_cast<unsigned>(plan.k_split));
@@ -2204,14 +2175,13 @@ void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *
         if (plan.waves == 2) {
             hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU, 2>), grid, dim3(2 * kThreads), 0, stream, packed,
                                static_cast<const T *>(x), static_cast<T *>(y), partial, counters,
-                               static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split,
-                               g_spin_limit.load());
+                               static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
             return;
         }
     }
     hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU>), grid, dim3(kThreads), 0, stream, packed,
                        static_cast<const T *>(x), static_cast<T *>(y), partial, counters, static_cast<int>(M),
-                       static_cast<int>(rows), G, plan.chunk_groups, plan.k_split, g_spin_limit.load());
+                       static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
 }
 
 template <typename T>
@@ -2240,8 +2210,8 @@ int launch_lut_once(const uint32_t *packed, const void *x, void *y, int64_t M, i
                     const LutPlan &plan, void *ws, hipStream_t stream, bool glu) {
     const int G = static_cast<int>(columns / kBlockWeights);
     unsigned *counters = plan.k_split > 1 ? static_cast<unsigned *>(ws) : nullptr;
-    uint64_t *partial =
-        plan.k_split > 1 ? reinterpret_cast<uint64_t *>(static_cast<char *>(ws) + plan.counter_bytes) : nullptr;
+    float *partial =
+        plan.k_split > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + plan.counter_bytes) : nullptr;
     if (glu) {  // SwiGLU epilogue: one vector per workgroup
 #define TQ1_LUT_GLU_CASE(CC)                                                                          \
         if (plan.chunk == CC && plan.batch_tile == 1) {                                               \

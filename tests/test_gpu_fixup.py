@@ -1,9 +1,9 @@
 """The in-launch split-K fix-ups: the M = 1 decode GEMV (LUT23 kernel, K
-chunks published as {value, flag} pieces and summed in chunk order by the last
-workgroup to arrive) at the 27B shapes and tall or ragged ones, against the
-fp64 oracle and the fp32 summation bound; exact integers; bit identity between
-runs; the bounded waits of the LUT23 and wide-GEMM fix-ups driven to give up
-from the host; two streams at once, each with its own workspace.
+chunks summed in chunk order by the last workgroup to arrive) at the 27B
+shapes and tall or ragged ones, against the fp64 oracle and the fp32
+summation bound; exact integers; bit identity between runs; the wide GEMM's
+bounded stream-K wait driven to give up from the host; two streams at once,
+each with its own workspace.
 
 Pinned by: the fp64 dense product (oracle_matmul, src/ternel_mlx/reference.py:
 171-177) with the per-case normalised tolerance of the north star; exact
@@ -78,7 +78,7 @@ def test_split_gemv_is_bit_identical_between_runs(rows: int, columns: int) -> No
     first = gemv(blocks, x, torch.float16)
     for _ in range(3):
         np.testing.assert_array_equal(gemv(blocks, x, torch.float16), first)
-    assert workspace_errors() and not any(workspace_errors().values())
+    assert not any(workspace_errors().values())
 
 
 def test_fused_swiglu_gemv_at_the_27b_mlp_width() -> None:
@@ -136,16 +136,6 @@ def _forced_give_up(run) -> int:
         check_workspaces()
     assert not any(workspace_errors().values())  # check_workspaces zeroed it again
     return words[0] if words else 0
-
-
-def test_a_lut_fixup_that_gives_up_is_reported_and_the_next_call_is_clean() -> None:
-    rows, columns = 17408, 5120
-    blocks = random_blocks(rows, columns, seed=41)
-    x = np.random.default_rng(41).normal(0, 1, size=(1, columns)).astype(np.float16)
-    packed, xt, lay = pack(blocks), to_dev(x), layout(rows, columns)
-    want = tq1_matmul_words(packed, xt, layout=lay).cpu()
-    assert _forced_give_up(lambda: tq1_matmul_words(packed, xt, layout=lay)) & 1
-    assert torch.equal(tq1_matmul_words(packed, xt, layout=lay).cpu(), want)
 
 
 def test_a_wide_reduction_that_gives_up_is_reported_and_the_next_call_is_clean() -> None:

@@ -228,16 +228,13 @@ def test_split_k_refusal_message() -> None:
 def test_workspace_queries() -> None:
     handle = _lib.lib()
     # every split workspace: a fixed 64 KiB counter region (its last word the
-    # error word), then the LUT23 kernel's fixed 32 MiB region of 64-bit piece
-    # slots; the other kernels' partials start past both
-    lut = 64 * 1024
-    counters = 64 * 1024 + 32 * 2**20
-    # LUT23 pieces: 8 bytes per (chunk, vector, row)
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 17408, 5120, 0, 0) == lut + 10 * 17408 * 8
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 17408, 0, 0) == lut + 17 * 5120 * 8
-    assert handle.ternel_tq1_swiglu_workspace_bytes(1, 34816, 5120, 0) == lut + 10 * 34816 * 8
+    # error word), then fp32 partials
+    counters = 64 * 1024
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 17408, 5120, 0, 0) == counters + 10 * 17408 * 4
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 17408, 0, 0) == counters + 17 * 5120 * 4
+    assert handle.ternel_tq1_swiglu_workspace_bytes(1, 34816, 5120, 0) == counters + 10 * 34816 * 4
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 1) == 0
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 8) == lut + 8 * 256 * 8
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 256, 5120, 1, 8) == counters + 8 * 256 * 4
     tile, direct = 1, 2
     assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, tile, 1) == 0
     assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, tile, 5) == counters + 5 * 8 * 256 * 4
