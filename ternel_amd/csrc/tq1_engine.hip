@@ -2047,6 +2047,9 @@ int check_geometry(int64_t M, int64_t rows, int64_t columns) {
 // Above this many K chunks the split-K fix-up costs more than the extra
 // workgroups buy (measured, see plan_lut).
 constexpr int64_t kLutMaxChunks = 20;
+// Split-K partials of one LUT23 launch, at most (a larger batch runs as more
+// launches).
+constexpr int64_t kLutPartialBytes = int64_t{256} << 20;
 
 // The split-K workspace starts with a fixed region of arrival counters, one per
 // (row block, batch tile), that is all-zero between calls. Fixing its size keeps
@@ -2158,6 +2161,21 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
     if (plan->batch_tiles > 65535) {
         plan->batch_tiles = 65535;
         plan->launch_vectors = std::min<int64_t>(plan->launch_vectors, 65535 * static_cast<int64_t>(plan->batch_tile));
+    }
+    if (plan->k_split > 1) {
+        // At most kLutPartialBytes of partials per launch: fewer vectors per
+        // launch, or -- when not even one batch tile fits and the split was
+        // automatic -- no split (a grid that tall fills the CUs unsplit).
+        const int64_t per_vector = static_cast<int64_t>(plan->k_split) * rows * sizeof(float);
+        int64_t fit = kLutPartialBytes / per_vector;
+        fit -= fit % plan->batch_tile;
+        if (fit < plan->batch_tile && k_split == 0) {
+            plan->k_split = 1;
+            plan->chunk_groups = static_cast<int>(G);
+        } else if (fit >= plan->batch_tile && plan->launch_vectors > fit) {
+            plan->launch_vectors = fit;
+            plan->batch_tiles = fit / plan->batch_tile;
+        }
     }
     plan->counter_bytes = plan->k_split > 1 ? kCounterRegionBytes : 0;
     plan->partial_bytes = plan->k_split > 1 ? static_cast<size_t>(plan->k_split) *

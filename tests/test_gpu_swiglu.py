@@ -66,8 +66,9 @@ def test_fused_swiglu_matches_the_unfused_layers(dtype, batch: int, hidden: int,
     want, gv, uv = unfused(gate_blocks, up_blocks, x, with_operands=True)
     diff = (got.float() - want.float()).abs()
     if (dtype == torch.float16 and batch > 4) or batch == 1:
-        # The fp16 GEMM path, and at one vector the stream GEMV, split a
-        # 2 x hidden weight differently from a hidden one, so the fp32 sums
+        # The fp16 GEMM path, and at one vector the LUT kernel's automatic
+        # K split (chosen from the row count), cut a 2 x hidden weight
+        # differently from a hidden one, so the fp32 sums
         # differ by up to the accumulation bound (columns x eps x |x||W|, per
         # operand) and may then round to another value of the activation type
         # (a step of either neighbouring binade); z moves by at most that
