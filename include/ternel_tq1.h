@@ -156,6 +156,24 @@ size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t column
                                          int k_split);
 
 /*
+ * ternel_tq1_matmul without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc); no counterpart in the reference. Same arguments, kernels and
+ * results as ternel_tq1_matmul; its split-K counters and partials live in a
+ * static device array of 64 KiB + 16 MiB that each device the library runs on
+ * holds until the process ends. Allocates nothing. A batch whose partials
+ * exceed 16 MiB runs as several launches; a requested k_split whose single
+ * batch tile needs more (k_split * batch_tile * rows * 4 bytes > 16 MiB) is
+ * rejected with TERNEL_TQ1_EINVAL, and an automatic split falls back to none.
+ * All calls on one device share the array: calls that overlap in time on a
+ * device (two streams, two threads) race. The first call on each device sets
+ * the array up (resolves its address, zeroes its counters on `stream`) and
+ * must not be under stream capture.
+ */
+int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
+                              int64_t columns, int dtype, int batch_tile, int k_split, void *stream);
+
+/*
  * MFMA product y = x @ W^T, fp16 activations, v_mfma_f32_32x32x16_f16 with fp32
  * accumulation, in one of three forms (the reference's GemmConfig forms,
  * src/ternel_mlx/kernels.py:1043-1188, re-chosen for CDNA4):

@@ -47,6 +47,7 @@ SIGNATURES = {
     "ternel_tq1_tiled_from_words": (_int, [_p, _i64, _i64, _i64, _p, _p, _p]),
     "ternel_tq1_matmul": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p, _size, _p]),
     "ternel_tq1_matmul_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
+    "ternel_tq1_matmul_noalloc": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p]),
     "ternel_tq1_gemm": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p, _size, _p]),
     "ternel_tq1_gemm_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
     "ternel_tq1_get_rows": (_int, [_p, _i64, _i64, _p, _i64, _p, _int, _p]),

@@ -2087,7 +2087,10 @@ bool lut_chunk_supported(int batch_tile, int chunk) {
 
 int device_cu_count();  // the current device's CUs (256 when it cannot be queried)
 
-int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split, LutPlan *plan) {
+// max_partial_bytes bounds one launch's split-K partials (kLutPartialBytes
+// unless the workspace is a fixed array).
+int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split, LutPlan *plan,
+             int64_t max_partial_bytes = kLutPartialBytes) {
     const int64_t G = columns / kBlockWeights;
     // Measured on MI355X: one vector per workgroup beats batch tiles of 2 and 4
     // at every 27B shape up to M = 4 (gate/up M=4: 18.3 us vs 20.3 and 25.8);
@@ -2163,11 +2166,11 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
         plan->launch_vectors = std::min<int64_t>(plan->launch_vectors, 65535 * static_cast<int64_t>(plan->batch_tile));
     }
     if (plan->k_split > 1) {
-        // At most kLutPartialBytes of partials per launch: fewer vectors per
+        // At most max_partial_bytes of partials per launch: fewer vectors per
         // launch, or -- when not even one batch tile fits and the split was
         // automatic -- no split (a grid that tall fills the CUs unsplit).
         const int64_t per_vector = static_cast<int64_t>(plan->k_split) * rows * sizeof(float);
-        int64_t fit = kLutPartialBytes / per_vector;
+        int64_t fit = max_partial_bytes / per_vector;
         fit -= fit % plan->batch_tile;
         if (fit < plan->batch_tile && k_split == 0) {
             plan->k_split = 1;
@@ -2598,6 +2601,54 @@ int launch_get_rows(const uint32_t *table, int64_t rows, int64_t columns, const 
     return TERNEL_TQ1_OK;
 }
 
+// The split-K workspace of ternel_tq1_matmul_noalloc as a file-scope device
+// array (counter region, then at most kNoAllocPartialBytes of fp32 partials),
+// for callers that cannot allocate. Each device the library runs on holds its
+// own copy until the process ends. In host code `scratch` is a stand-in, not
+// a device address: kernels and copies only ever see the address resolved
+// per device by noalloc_scratch().
+constexpr int64_t kNoAllocPartialBytes = int64_t{16} << 20;
+constexpr size_t kNoAllocScratchBytes = kCounterRegionBytes + kNoAllocPartialBytes;
+static __device__ __align__(256) unsigned scratch[kNoAllocScratchBytes / sizeof(unsigned)];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_address[kScratchDevices];  // per device; null until resolved
+
+// This device's copy of `scratch`. The first call on a device resolves its
+// address and zeroes its counter region on `stream` (stream-ordered before the
+// launch that follows); the LUT23 fix-up leaves every counter it used at zero,
+// so the region stays zero between calls. The set-up call may not be under
+// stream capture.
+int noalloc_scratch(hipStream_t stream, void **out) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return fail(TERNEL_TQ1_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (device < 0 || device >= kScratchDevices)
+        return fail(TERNEL_TQ1_EINVAL, "device %d is past the %d whose scratch addresses are kept", device,
+                    kScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_address[device]) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        if ((e = hipStreamIsCapturing(stream, &capture)) != hipSuccess)
+            return fail(TERNEL_TQ1_EHIP, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+        if (capture != hipStreamCaptureStatusNone)
+            return fail(TERNEL_TQ1_EINVAL,
+                        "the first ternel_tq1_matmul_noalloc call on device %d is under stream capture; make one "
+                        "call outside capture first (it sets up the device's scratch)",
+                        device);
+        void *address = nullptr;
+        if ((e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch))) != hipSuccess)
+            return fail(TERNEL_TQ1_EHIP, "resolving the scratch array on device %d: %s", device,
+                        hipGetErrorString(e));
+        if ((e = hipMemsetAsync(address, 0, kCounterRegionBytes, stream)) != hipSuccess)
+            return fail(TERNEL_TQ1_EHIP, "clearing the scratch counters: %s", hipGetErrorString(e));
+        g_scratch_address[device] = address;
+    }
+    *out = g_scratch_address[device];
+    return TERNEL_TQ1_OK;
+}
+
 extern "C" {
 
 const char *ternel_tq1_last_error(void) { return g_last_error; }
@@ -2797,6 +2848,37 @@ int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M,
         return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
                     need);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case TERNEL_TQ1_F16:
+            return launch_lut<_Float16>(packed, x, y, M, rows, columns, plan, ws, s);
+        case TERNEL_TQ1_BF16:
+            return launch_lut<bf16_t>(packed, x, y, M, rows, columns, plan, ws, s);
+        default:
+            return launch_lut<float>(packed, x, y, M, rows, columns, plan, ws, s);
+    }
+}
+
+int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
+                              int64_t columns, int dtype, int batch_tile, int k_split, void *stream) {
+    g_last_error[0] = '\0';
+    int rc;
+    if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
+    if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
+    LutPlan plan;
+    if ((rc = plan_lut(M, rows, columns, batch_tile, k_split, &plan, kNoAllocPartialBytes)) != TERNEL_TQ1_OK)
+        return rc;
+    if (plan.partial_bytes > static_cast<size_t>(kNoAllocPartialBytes))
+        return fail(TERNEL_TQ1_EINVAL,
+                    "a k split of %d over %lld rows needs %lld bytes of partials per batch tile of %d, more than "
+                    "the %lld bytes of the static scratch",
+                    plan.k_split, static_cast<long long>(rows),
+                    static_cast<long long>(plan.k_split) * plan.batch_tile * rows * static_cast<long long>(sizeof(float)),
+                    plan.batch_tile, static_cast<long long>(kNoAllocPartialBytes));
+    if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+    if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    void *ws = nullptr;
+    if (plan.k_split > 1 && (rc = noalloc_scratch(s, &ws)) != TERNEL_TQ1_OK) return rc;
     switch (dtype) {
         case TERNEL_TQ1_F16:
             return launch_lut<_Float16>(packed, x, y, M, rows, columns, plan, ws, s);
