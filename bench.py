@@ -55,7 +55,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-model-stream", action="store_true")
     p.add_argument("--no-small-batch", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--cpu-seconds", type=float, default=20.0)
     p.add_argument("--stream-ceiling", action="store_true",
                    help="measure the single-launch HBM read ceiling (libternel_probe.so) at the configs' matrix "
                         "sizes and print one JSON line")
@@ -99,9 +99,24 @@ def blas_threads() -> int:
     return os.cpu_count() or 1
 
 
+def timed_calls(fn, seconds: float, min_calls: int = 1) -> tuple[int, float]:
+    """Calls fn() until `seconds` have elapsed (at least min_calls): (calls, elapsed s)."""
+    calls = 0
+    start = time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= seconds and calls >= min_calls:
+            return calls, elapsed
+
+
 def cpu_baseline(seconds: float) -> dict:
-    """The reference's CPU path (decode_tq1_blocks + numpy matmul), restated in the
-    oracle, timed on a bounded sample: whole gate/up matrix decodes + matvecs."""
+    """The reference's CPU path, restated in the oracle, timed on a bounded sample
+    whole gate/up decode + fp32 numpy matvec (the reported
+    value, about half of `seconds`), the matvec alone over the pre-decoded matrix,
+    and at configs[0] (4096 x 4096) decode + matvec and the literal per-row
+    _reference_gemv restatement (src/bonsai_tq1/reference.py:14-65)."""
     import numpy as np
 
     from oracle import tq1_oracle as O
@@ -110,15 +125,19 @@ def cpu_baseline(seconds: float) -> dict:
     name, K, N = C1_SHAPES[0]
     blocks = synthetic.host_blocks(N, K, seed=synthetic.SEED_BASE + 1)
     x = synthetic.host_activations(1, K, seed=synthetic.SEED_BASE + 1)
-    calls = 0
-    start = time.perf_counter()
-    while True:
-        O.cpu_decode_matmul(blocks, x, rows=N, columns=K)
-        calls += 1
-        elapsed = time.perf_counter() - start
-        if elapsed >= seconds:
-            break
+    calls, elapsed = timed_calls(lambda: O.cpu_decode_matmul(blocks, x, rows=N, columns=K), 0.5 * seconds)
     per_call = elapsed / calls
+    dense = O.cpu_decode(blocks, rows=N, columns=K)
+    mm_calls, mm_elapsed = timed_calls(lambda: O.cpu_matmul(dense, x), 0.15 * seconds)
+    del dense, blocks
+
+    K0 = N0 = 4096
+    blocks0 = synthetic.host_blocks(N0, K0, seed=synthetic.SEED_BASE + 0)
+    x0 = synthetic.host_activations(1, K0, seed=synthetic.SEED_BASE + 0)
+    c0_calls, c0_elapsed = timed_calls(lambda: O.cpu_decode_matmul(blocks0, x0, rows=N0, columns=K0), 0.15 * seconds)
+    g0_calls, g0_elapsed = timed_calls(
+        lambda: O.reference_gemv(blocks0, x0[0].astype(np.float32), rows=N0, columns=K0), 0.2 * seconds)
+    bytes0 = packed_bytes(K0, N0)
     return {
         "value": round(packed_bytes(K, N) / per_call / 1e9, 4),
         "unit": "GB/s",
@@ -128,6 +147,17 @@ def cpu_baseline(seconds: float) -> dict:
                    f"{name} matrix K={K} N={N} ({packed_bytes(K, N)} packed bytes), {elapsed:.1f} s; "
                    f"decode is single-threaded numpy, the matvec uses the BLAS threads"),
         "seconds_per_call": round(per_call, 4),
+        "matmul_only": {"calls": mm_calls, "ms_per_call": round(mm_elapsed / mm_calls * 1e3, 3),
+                        "packed_GB/s": round(packed_bytes(K, N) / (mm_elapsed / mm_calls) / 1e9, 3),
+                        "dense_fp32_GB/s": round(4 * K * N / (mm_elapsed / mm_calls) / 1e9, 2),
+                        "what": f"fp32 numpy matvec over the pre-decoded dense {name} W (BLAS threads)"},
+        "config0": {"workload": "configs[0]: M=1, K=N=4096, fp16 activations",
+                    "decode_matmul_ms": round(c0_elapsed / c0_calls * 1e3, 2),
+                    "decode_matmul_GB/s": round(bytes0 / (c0_elapsed / c0_calls) / 1e9, 4),
+                    "reference_gemv_ms": round(g0_elapsed / g0_calls * 1e3, 2),
+                    "reference_gemv_GB/s": round(bytes0 / (g0_elapsed / g0_calls) / 1e9, 4),
+                    "calls": {"decode_matmul": c0_calls, "reference_gemv": g0_calls},
+                    "reference_gemv_is": "per-row decode, fp32 group dots, fp32 scale sum, single-threaded"},
         "cpu_model": cpu_model(),
         "os_cpu_count": os.cpu_count(),
     }
@@ -152,10 +182,13 @@ def trace_summary(path: str) -> int:
                 continue
             key = (row["Kernel_Name"], row["Grid_Size_X"], row["Grid_Size_Y"], row["Grid_Size_Z"])
             groups.setdefault(key, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
-    print(f"{'calls':>6} {'avg_us':>9} {'median_us':>9} {'min_us':>8} {'max_us':>8}  grid (x,y,z)  kernel")
+    print(f"{'calls':>6} {'avg_us':>9} {'p5_us':>8} {'median_us':>9} {'p95_us':>8} {'min_us':>8} {'max_us':>8}  "
+          f"grid (x,y,z)  kernel")
     for (name, gx, gy, gz), ns in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        print(f"{len(ns):6d} {statistics.fmean(ns) / 1e3:9.3f} {statistics.median(ns) / 1e3:9.3f} "
-              f"{min(ns) / 1e3:8.3f} {max(ns) / 1e3:8.3f}  ({gx},{gy},{gz})  {name[:110]}")
+        ns = sorted(ns)
+        p5, p95 = ns[int(round(0.05 * (len(ns) - 1)))], ns[int(round(0.95 * (len(ns) - 1)))]
+        print(f"{len(ns):6d} {statistics.fmean(ns) / 1e3:9.3f} {p5 / 1e3:8.3f} {statistics.median(ns) / 1e3:9.3f} "
+              f"{p95 / 1e3:8.3f} {ns[0] / 1e3:8.3f} {ns[-1] / 1e3:8.3f}  ({gx},{gy},{gz})  {name[:110]}")
     return 0
 
 
@@ -309,7 +342,9 @@ def main() -> int:
     torch.cuda.synchronize()
     launch_ms = sorted(a.elapsed_time(b) for a, b in pairs)
     mean_launch_ms = sum(launch_ms) / len(launch_ms)
-    median_launch_ms = launch_ms[len(launch_ms) // 2]
+
+    def quantile(q: float) -> float:  # nearest rank over the sorted launches
+        return launch_ms[min(len(launch_ms) - 1, int(round(q * (len(launch_ms) - 1))))]
     per_matrix = {}
     for i, (name, K, N) in enumerate(C1_SHAPES):
         g = graph_of(lambda i=i: [tq1_matmul_words(weights[s % ring][i], xs[i], layout=layouts[i], config=config)
@@ -377,7 +412,10 @@ def main() -> int:
             "mean_launch_us": round(graph_launch_ms * 1e3, 3),
             "timing": f"{args.steps} cold launches back to back in one HIP graph, events on the launch stream",
             "eager_event_pair_mean_us": round(mean_launch_ms * 1e3, 3),
-            "eager_event_pair_median_us": round(median_launch_ms * 1e3, 3),
+            "eager_event_pair_us": {"p5": round(quantile(0.05) * 1e3, 3), "median": round(quantile(0.5) * 1e3, 3),
+                                    "p95": round(quantile(0.95) * 1e3, 3), "launches": len(launch_ms),
+                                    "timing": "one event pair around each eager launch (dispatch included), "
+                                              "as the reference's per-launch statistics"},
             "traffic_detail": traffic,
         },
     }

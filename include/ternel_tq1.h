@@ -28,7 +28,9 @@
  * reorder the reference applies before its fast kernels
  * (src/bonsai_tq1/lut23_reorder.py:126-165, src/ternel_mlx/packing.py:51-83).
  * Compute kernels assume validated bytes; on illegal bytes they stay
- * memory-safe but their arithmetic is undefined.
+ * memory-safe (every byte value's table entries and digits stay in range,
+ * checked exhaustively by tests/test_byte_bounds.py) but their arithmetic is
+ * undefined.
  *
  * Activations x are [M][columns] row-major, outputs y are [M][rows] row-major,
  * both of `dtype` (TERNEL_TQ1_F16 is the graded type; BF16/F32 also accepted by

@@ -179,12 +179,6 @@ def restore_tensor_arrays(codes: np.ndarray, scales: np.ndarray, rows: int, *, t
     return out
 
 
-def scales_as_float(blocks: np.ndarray, dtype=np.float32) -> np.ndarray:
-    """Raw little-endian fp16 scale bits -> float; src/bonsai_tq1/reference.py:9-11."""
-    packed = _as_blocks(blocks)
-    return np.ascontiguousarray(packed[:, :2]).view("<f2").reshape(-1).astype(dtype)
-
-
 def reference_gemv(blocks, activation, *, rows: int, columns: int) -> np.ndarray:
     """Per-row decode-then-dot fp32 GEMV; src/bonsai_tq1/reference.py:14-39,55-65.
 
@@ -363,16 +357,26 @@ def compare(candidate, reference) -> dict:
     }
 
 
-def cpu_decode_matmul(blocks, x, *, rows: int, columns: int) -> np.ndarray:
-    """The BASELINE CPU arm: whole-matrix decode -> dense fp32 W -> ``x @ W.T`` -> fp16.
+def cpu_decode(blocks, *, rows: int, columns: int) -> np.ndarray:
+    """The BASELINE CPU arm's decode: whole-matrix decode -> dense fp32 W = (t-1)*scale.
 
-    Restates the reference's "Python decoder + numpy matmul" path
-    (src/bonsai_tq1/format.py:94-122 then src/ternel_mlx/reference.py:155-177 in fp32).
-    Timed by ``bench.py`` as the reported CPU baseline; never used by the product.
+    Restates the reference's Python decoder (src/bonsai_tq1/format.py:94-122,
+    validating) and densification (src/ternel_mlx/reference.py:155-168) in fp32.
+    Timed by ``bench.py`` as part of the reported CPU baseline; never used by the product.
     """
     flat = np.asarray(blocks, dtype=np.uint8).reshape(-1, BLOCK_BYTES)
     scale_bits, trits = decode_tq1_blocks(flat, validate=True)
     weights = trits.astype(np.float32) - np.float32(1.0)
     weights *= np.ascontiguousarray(scale_bits).view("<f2").astype(np.float32).reshape(-1, 1)
-    dense = weights.reshape(rows, columns)
+    return weights.reshape(rows, columns)
+
+
+def cpu_matmul(dense: np.ndarray, x) -> np.ndarray:
+    """The BASELINE CPU arm's product: ``x @ W.T`` in fp32 (numpy BLAS) -> fp16;
+    src/ternel_mlx/reference.py:171-177 at the reference's fp32 CPU precision."""
     return (np.asarray(x, dtype=np.float32) @ dense.T).astype(np.float16)
+
+
+def cpu_decode_matmul(blocks, x, *, rows: int, columns: int) -> np.ndarray:
+    """The BASELINE CPU arm end to end: ``cpu_decode`` then ``cpu_matmul``."""
+    return cpu_matmul(cpu_decode(blocks, rows=rows, columns=columns), x)

@@ -37,6 +37,7 @@
 #include <type_traits>
 
 #include "ternel_tq1.h"
+#include "tq1_bytes.h"
 
 namespace {
 
@@ -45,20 +46,19 @@ constexpr int kBlockWeights = 128;
 constexpr int kBlockBytes = 28;
 constexpr int kBlockWords = 7;
 constexpr int kCodeSlots = 26;
-constexpr int kFullSlots = 25;
-constexpr uint32_t kMaxTailByte = 26;
+using tq1_bytes::kFullSlots;
+using tq1_bytes::kMaxTailByte;
 
 // Packed layout: 64-row tiles, 7 words per block.
 constexpr int kTileRows = 64;
 constexpr int kTileGroupWords = kBlockWords * kTileRows;  // 448 words per (tile, group)
 
-// LUT23 tables of one 128-weight group, fp32: L2[25][9] over trits (0,1) of a
-// slot, L3[25][27] over trits (2,3,4), tail[27] over trits 125..127.
-constexpr int kL2Entries = 9;
-constexpr int kL3Entries = 27;
-constexpr int kL3Base = kFullSlots * kL2Entries;             // 225
-constexpr int kTailBase = kL3Base + kFullSlots * kL3Entries;  // 900
-constexpr int kLutFloats = kTailBase + 27;                    // 927
+// LUT23 tables of one 128-weight group (geometry in tq1_bytes.h).
+using tq1_bytes::kL2Entries;
+using tq1_bytes::kL3Entries;
+using tq1_bytes::kL3Base;
+using tq1_bytes::kTailBase;
+using tq1_bytes::kLutFloats;
 constexpr int kTasksPerGroup = 2 * kFullSlots + 1;            // L2 x25, L3 x25, tail
 
 constexpr int kThreads = 256;
@@ -419,16 +419,7 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
                                                             int64_t n_ids, T *__restrict__ out,
                                                             int vector_out) {
     __shared__ uint32_t digits[256];  // byte b -> its digits, digit i in bits 2i..2i+1
-    {
-        uint32_t b = threadIdx.x, d = 0;
-#pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const uint32_t q = b / 3u;
-            d |= (b - 3u * q) << (2 * i);
-            b = q;
-        }
-        digits[threadIdx.x] = d;
-    }
+    digits[threadIdx.x] = tq1_bytes::byte_digits(threadIdx.x);
     __syncthreads();
     const int64_t per_token = static_cast<int64_t>(G) * kGatherRuns;
     const int64_t total = n_ids * per_token;
@@ -477,7 +468,7 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
                     pk[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e]))) |
                             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e + 1]))) << 16);
                 // Non-temporal: a wave's store is one contiguous 1 KiB that no
-                // cache needs (8192-token fp16 gather 25.0 -> 22.0 us on MI355X;
+                // cache needs (8192-token fp16 gather 25.4 -> 21.7 us on MI355X;
                 // the fp32 form's two 16-byte stores per lane, 32 bytes apart,
                 // measured 45 -> 70 us that way, so they keep plain stores).
                 __builtin_nontemporal_store(gather_u32x4{pk[0], pk[1], pk[2], pk[3]},
@@ -625,8 +616,8 @@ __device__ __forceinline__ uint32_t lut_address_hi(uint32_t pair, uint32_t base)
 __device__ __forceinline__ void split_pair(uint32_t pair, uint32_t base, uint32_t &lo_a, uint32_t &hi_a,
                                            uint32_t &lo_b, uint32_t &hi_b) {
     const u16x2 p = __builtin_bit_cast(u16x2, pair);
-    const u16x2 h = (p * static_cast<unsigned short>(57)) >> static_cast<unsigned short>(9);
-    const u16x2 l = p - h * static_cast<unsigned short>(9);
+    const u16x2 h = tq1_bytes::lut23_high(p);
+    const u16x2 l = tq1_bytes::lut23_low(p, h);
     const uint32_t hb = __builtin_bit_cast(uint32_t, h), lb = __builtin_bit_cast(uint32_t, l);
     lo_a = lut_address_lo(lb, base);
     hi_a = lut_address_lo(hb, base);
@@ -791,7 +782,7 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
                 }
             }
             const float scale = half_bits_to_float(w[c][0]);
-            const uint32_t tail = lut_base + 4 * min(w[c][6] >> 24, kMaxTailByte);
+            const uint32_t tail = lut_base + 4 * tq1_bytes::tail_entry(w[c][6] >> 24);
 #pragma unroll
             for (int j = 0; j < BT; ++j) {
                 sum[j] += table(tail, j, c, kTailBase);
@@ -933,17 +924,8 @@ constexpr int kGemmStride = kBlockWeights + 8;  // halves per LDS row
 // each t = (t mod 2^24) * 3 leaves the next base-3 digit, most significant
 // first, in bits 24-25 (exact for every legal byte; the tail byte p <= 26 uses
 // 9 * 69043). Two carriers become two fp16 weights with two v_perm_b32.
-constexpr uint32_t kByteDigitScale = 69043u;          // ~2^24 / 243
-constexpr uint32_t kTailDigitScale = 9u * 69043u;     // ~2^24 / 27
-
-__device__ __forceinline__ void byte_digit_carriers(uint32_t p, uint32_t (&d)[5]) {
-    uint32_t t = __umul24(p, kByteDigitScale);
-#pragma unroll
-    for (int i = 4; i >= 0; --i) {
-        t = __umul24(t, 3u);
-        d[i] = t;  // digit i (weight 3^i) in bits 24-25
-    }
-}
+using tq1_bytes::byte_digit_carriers;
+using tq1_bytes::tail_digit_carriers;
 
 // {-s, z, +s} selected by digit d: selector bytes (2d, 2d+1) per fp16, from a
 // pair of carriers' top bytes. z is 0, or NaN when the scale is inf/NaN, so that
@@ -976,12 +958,11 @@ __device__ __forceinline__ void decode_half_block(const uint32_t (&w)[kBlockWord
         if (sl < kFullSlots) {
             byte_digit_carriers(p, d);
         } else {
-            uint32_t t = __umul24(p, kTailDigitScale);
-#pragma unroll
-            for (int i = 2; i >= 0; --i) {
-                t = __umul24(t, 3u);
-                d[i] = t;
-            }
+            uint32_t dt[3];
+            tail_digit_carriers(p, dt);
+            d[0] = dt[0];
+            d[1] = dt[1];
+            d[2] = dt[2];
             d[3] = d[4] = 0u;
         }
 #pragma unroll
@@ -1188,14 +1169,12 @@ __device__ __forceinline__ void direct_step(float16v (&acc)[NB], const uint32_t 
             const uint32_t w6 = upper ? u[3] : other;
             uint32_t d24[5];
             byte_digit_carriers((w6 >> 16) & 0xffu, d24);
-            uint32_t t = __umul24(w6 >> 24, kTailDigitScale);
-            const uint32_t t2 = t = __umul24(t, 3u);
-            const uint32_t t1 = t = __umul24(t, 3u);
-            const uint32_t t0 = __umul24(t, 3u);
+            uint32_t dt[3];
+            tail_digit_carriers(w6 >> 24, dt);
             c[60] = upper ? d24[4] : d24[0];
-            c[61] = upper ? t0 : d24[1];
-            c[62] = upper ? t1 : d24[2];
-            c[63] = upper ? t2 : d24[3];
+            c[61] = upper ? dt[0] : d24[1];
+            c[62] = upper ? dt[1] : d24[2];
+            c[63] = upper ? dt[2] : d24[3];
         }
 #pragma unroll
         for (int p = 4 * st; p < 4 * st + 4; ++p) a_dec[p] = weight_pair(c[2 * p], c[2 * p + 1], table_hi, table_lo);
@@ -1725,14 +1704,12 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                 const uint32_t w6 = upper ? w[3] : w[4];
                 uint32_t d24[5];
                 byte_digit_carriers((w6 >> 16) & 0xffu, d24);
-                uint32_t t = __umul24(w6 >> 24, kTailDigitScale);
-                const uint32_t t2 = t = __umul24(t, 3u);
-                const uint32_t t1 = t = __umul24(t, 3u);
-                const uint32_t t0 = __umul24(t, 3u);
+                uint32_t dt[3];
+                tail_digit_carriers(w6 >> 24, dt);
                 c[60] = upper ? d24[4] : d24[0];
-                c[61] = upper ? t0 : d24[1];
-                c[62] = upper ? t1 : d24[2];
-                c[63] = upper ? t2 : d24[3];
+                c[61] = upper ? dt[0] : d24[1];
+                c[62] = upper ? dt[1] : d24[2];
+                c[63] = upper ? dt[2] : d24[3];
             }
 #pragma unroll
             for (int q = 4 * st; q < 4 * st + 4; ++q) a[q] = weight_pair(c[2 * q], c[2 * q + 1], th, tl);
