@@ -470,17 +470,20 @@ def main() -> int:
     return 0
 
 
-PHASES = ("start", "own tables written", "tables ready (barrier)", "blocks summed", "partial stored and acknowledged",
-          "arrival counted", "fix-up done")
+PHASES = ("start", "activations arrived", "first words issued", "own tables written", "tables ready (barrier)",
+          "blocks summed", "partial stored and acknowledged", "arrival counted", "fix-up done")
 
 
 def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedTensorLayout, MatmulConfig,
                   graph_of, time_graph) -> int:
     """Per configs[1] matrix: three cold launches of the M=1 GEMV (the LUT23
-    kernel) with the phase stamps of every wave (100 MHz wall clock, lane 0):
-    each phase's time after the launch's first wave started, and -- free of
-    any clock offset between XCDs -- each phase's duration per wave; beside
-    them the graph-timed GEMV of the same build over the cold ring."""
+    kernel) with the phase stamps of every wave (100 MHz wall clock, lane 0)
+    and the XCC it ran on. Wall clocks of different XCCs are not comparable,
+    so every time is taken against the first wave start of the wave's own
+    XCC: each phase's time, the XCC's span (first start to last stamp), each
+    phase's duration per wave, and the time to the tables by the quarter of
+    the XCC's waves a wave started in; beside them the graph-timed GEMV of
+    the same build over a cold ring."""
     import ctypes
     import statistics
 
@@ -491,8 +494,15 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedT
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     max_waves = 8192
-    buf = (ctypes.c_ulonglong * (max_waves * len(PHASES) + max_waves * 2))()
+    slots = 16  # the phases, then (last slot) 1 + the XCC id
+    buf = (ctypes.c_ulonglong * (max_waves * slots))()
     ring = 14
+
+    def quantiles(values: list) -> dict:
+        values = sorted(values)
+        return {"median_us": round(statistics.median(values), 2),
+                "p95_us": round(values[int(0.95 * (len(values) - 1))], 2), "max_us": round(values[-1], 2)}
+
     for i, (name, K, N) in enumerate(C1_SHAPES):
         lay = PackedTensorLayout.for_tensor(N, K)
         weights = [pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
@@ -500,42 +510,43 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedT
         x = synthetic.device_activations(1, K, seed=synthetic.SEED_BASE + 1 + i)
         graph_ms = time_graph(graph_of(lambda: [tq1_matmul_words(weights[r % ring], x, layout=lay)
                                                 for r in range(ring * 4)])) / (ring * 4)
-        rows = []
+        phase_times = {phase: [] for phase in PHASES}
+        spans, durations, by_start = [], {}, [[] for _ in range(4)]
         for r in range(3):  # three cold launches, each over a copy last read 13 launches ago
             fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
             tq1_matmul_words(weights[(r + 5) % ring], x, layout=lay)
             waves = fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
-            stamps = [[buf[w * 8 + p] for p in range(len(PHASES))] for w in range(waves)]
-            stamps = [st for st in stamps if st[0]]
-            t0 = min(st[0] for st in stamps)
-            last_stamps, t0_last = stamps, t0
-            rows.append({PHASES[p]: [(st[p] - t0) * 10 / 1000 for st in stamps if st[p]] for p in range(len(PHASES))})
-        summary = {}
-        for p, phase in enumerate(PHASES):
-            values = [v for row in rows for v in row[phase]]
-            if values:
-                values.sort()
-                summary[phase] = {"min_us": round(values[0], 2),
-                                  "median_us": round(statistics.median(values), 2),
-                                  "p95_us": round(values[int(0.95 * (len(values) - 1))], 2),
-                                  "max_us": round(values[-1], 2)}
-        # Offset-free figures (a wave's own stamps): each phase's duration per
-        # wave, and how far apart the waves of one workgroup started.
-        durations = {}
-        for p in range(1, len(PHASES)):
-            d = sorted((st[p] - st[p - 1]) / 100 for st in last_stamps if st[p] and st[p - 1])
-            if d:
-                durations[f"{PHASES[p - 1]} -> {PHASES[p]}"] = {
-                    "median_us": round(statistics.median(d), 2), "p95_us": round(d[int(0.95 * (len(d) - 1))], 2)}
-        spreads = sorted((max(st[0] for st in last_stamps[g:g + 8]) - min(st[0] for st in last_stamps[g:g + 8])) / 100
-                         for g in range(0, len(last_stamps) - 7, 8))
-        print(json.dumps({"phase_profile": name, "K": K, "N": N, "waves": len(rows[0]["start"]),
-                          "gemv_graph_us": round(graph_ms * 1e3, 3),
-                          "phases_after_first_wave_start": summary,
-                          "phase_durations_per_wave": durations,
-                          "workgroup_start_spread_us (8-wave groups)": {"median": round(statistics.median(spreads), 2),
-                                                                        "max": round(spreads[-1], 2)},
-                          "clock": "s_memrealtime (100 MHz), lane 0 of every wave, 3 cold launches"}), flush=True)
+            stamps = [[buf[w * slots + p] for p in range(slots)] for w in range(waves)]
+            stamps = [st for st in stamps if st[0] and st[slots - 1]]
+            for xcc in {st[slots - 1] for st in stamps}:
+                mine = [st for st in stamps if st[slots - 1] == xcc]
+                t0 = min(st[0] for st in mine)
+                spans.append(max(max(v for v in st[:len(PHASES)] if v) for st in mine) / 100 - t0 / 100)
+                for p, phase in enumerate(PHASES):
+                    phase_times[phase] += [(st[p] - t0) / 100 for st in mine if st[p]]
+                ranked = sorted(mine, key=lambda st: st[0])
+                quarter = max(1, len(ranked) // 4)
+                for q in range(4):
+                    part = ranked[q * quarter:(q + 1) * quarter] if q < 3 else ranked[3 * quarter:]
+                    by_start[q] += [((st[0] - t0) / 100, (st[3] - st[0]) / 100, (st[1] - st[0]) / 100,
+                                     (st[2] - st[1]) / 100) for st in part if st[3] and st[1] and st[2]]
+            for p in range(1, len(PHASES)):
+                durations.setdefault(f"{PHASES[p - 1]} -> {PHASES[p]}", []).extend(
+                    (st[p] - st[p - 1]) / 100 for st in stamps if st[p] and st[p - 1])
+        print(json.dumps({
+            "phase_profile": name, "K": K, "N": N, "waves_per_launch": len(phase_times["start"]) // 3,
+            "gemv_graph_us": round(graph_ms * 1e3, 3),
+            "xcc_span_us": quantiles(spans),
+            "phases_after_xcc_first_wave_start": {ph: quantiles(v) for ph, v in phase_times.items() if v},
+            "phase_durations_per_wave": {k: quantiles(v) for k, v in durations.items() if v},
+            "tables_by_start_quarter": [
+                {"started_after_xcc_first_us": round(statistics.median(v[0] for v in part), 2),
+                 "start_to_tables_written_us": round(statistics.median(v[1] for v in part), 2),
+                 "start_to_activations_us": round(statistics.median(v[2] for v in part), 2),
+                 "activations_to_words_issued_us": round(statistics.median(v[3] for v in part), 2)}
+                for part in by_start if part],
+            "clock": "s_memrealtime (100 MHz), lane 0 of every wave, grouped by HW_REG_XCC_ID, 3 cold launches"}),
+            flush=True)
         del weights
     return 0
 

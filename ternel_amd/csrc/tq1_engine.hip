@@ -59,7 +59,6 @@ using tq1_bytes::kL3Entries;
 using tq1_bytes::kL3Base;
 using tq1_bytes::kTailBase;
 using tq1_bytes::kLutFloats;
-constexpr int kTasksPerGroup = 2 * kFullSlots + 1;            // L2 x25, L3 x25, tail
 
 constexpr int kThreads = 256;
 
@@ -72,7 +71,7 @@ constexpr int kWorkspaceErrorSlot = kWorkspaceCounterBytes / 4 - 1;
 // library that bench.py --phase-profile loads): lane 0 of each wave of the
 // M = 1 stream GEMV writes the 100 MHz wall clock at its phase boundaries.
 constexpr int kPhaseWaves = 8192;
-constexpr int kPhaseSlots = 8;
+constexpr int kPhaseSlots = 16;
 #ifdef TERNEL_TQ1_PROFILE
 __device__ unsigned long long g_phase_stamps[kPhaseWaves][kPhaseSlots];
 #define TQ1_PHASE(wave_id, slot)                                                                     \
@@ -82,7 +81,19 @@ __device__ unsigned long long g_phase_stamps[kPhaseWaves][kPhaseSlots];
             g_phase_stamps[(wave_id)][(slot)] = static_cast<unsigned long long>(wall_clock64());      \
         __builtin_amdgcn_sched_barrier(0);                                                           \
     } while (0)
+// The last slot holds 1 + the XCC the wave runs on (wall clocks of waves on
+// different XCCs are not comparable).
+#define TQ1_PHASE_XCC(wave_id)                                                                       \
+    do {                                                                                             \
+        unsigned xcc;                                                                                \
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));                           \
+        if ((threadIdx.x & 63) == 0 && (wave_id) < kPhaseWaves)                                      \
+            g_phase_stamps[(wave_id)][kPhaseSlots - 1] = 1ull + (xcc & 0xfu);                        \
+    } while (0)
 #else
+#define TQ1_PHASE_XCC(wave_id) \
+    do {                       \
+    } while (0)
 #define TQ1_PHASE(wave_id, slot) \
     do {                         \
     } while (0)
@@ -506,92 +517,116 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
 // Illegal regular bytes index inside the group's 927 entries and the tail is
 // clamped, so no input reads outside the tables.
 // ---------------------------------------------------------------------------
-// Table tasks of one sub-chunk: 51 per (vector, group). A thread owns tasks
-// tid, tid + 256, ...; it loads their activations before anything else so the
-// in-order vmcnt wait of the build never waits behind the weight stream.
 // Blocks whose words are in flight ahead of the one being consumed.
 constexpr int kLutLoadAhead = 2;
-// Offset in the group of table task k's first activation; its second is the
-// next one, its third the one after that (L3 slots and the tail; L2 slots
-// repeat the second).
-__device__ __forceinline__ int lut_task_base(int k) {
-    return k < kFullSlots ? 5 * k : (k < 2 * kFullSlots ? 5 * (k - kFullSlots) + 2 : 125);
-}
 
-constexpr int lut_task_count(int c, int bt) { return bt * c * kTasksPerGroup; }
-constexpr int lut_task_iters(int c, int bt, int threads) { return (lut_task_count(c, bt) + threads - 1) / threads; }
-
+// The sub-chunk's activations (BT vectors x C groups), copied to LDS with
+// 16-byte loads (element loads for rows that are not 16-byte aligned): a
+// workgroup asks for each of their cache lines once, where per-task gathers
+// ask for every line several times (gate/up M=1 9.39 -> 9.28 us on MI355X).
+// issue() loads them into registers -- every thread issues its loads, extra
+// threads repeating the last piece, so no load sits behind a branch -- and
+// store() writes them to LDS once they have arrived.
 template <typename T, int C, int BT, int NT>
-__device__ __forceinline__ void load_lut_inputs(T (&xv)[lut_task_iters(C, BT, NT)][3], const T *__restrict__ x,
-                                                int64_t K, int M, int b0, int g0, int tid) {
+struct ActivationCopy {
+    static constexpr int kRow = C * kBlockWeights;
+    static constexpr int kVec = 16 / static_cast<int>(sizeof(T));
+    static constexpr int kPieces = BT * kRow / kVec;
+    static constexpr int kIters = (kPieces + NT - 1) / NT;
+    static constexpr int kElemIters = (BT * kRow + NT - 1) / NT;
+    uint4 v[kIters];
+    T e[kElemIters];
+    bool aligned;
+
+    __device__ __forceinline__ void issue(const T *__restrict__ x, int64_t K, int M, int b0, int g0, int tid) {
+        aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+        if (aligned) {
 #pragma unroll
-    for (int it = 0; it < lut_task_iters(C, BT, NT); ++it) {
-        // Clamped rather than skipped: every load issues unconditionally, which
-        // keeps the compiler's vmcnt accounting exact (no branch around loads).
-        const int task = min(tid + it * NT, lut_task_count(C, BT) - 1);
-        const int j = task / (C * kTasksPerGroup);
-        const int rem = task - j * (C * kTasksPerGroup);
-        const int c = rem / kTasksPerGroup;
-        const int k = rem - c * kTasksPerGroup;
-        const int sample = min(b0 + j, M - 1);
-        const T *xg = x + static_cast<int64_t>(sample) * K + static_cast<int64_t>(g0 + c) * kBlockWeights;
-        // Kept raw: converting here would make the loads wait before the weight loads issue.
-        const int base = lut_task_base(k);
-        xv[it][0] = xg[base];
-        xv[it][1] = xg[base + 1];
-        xv[it][2] = xg[k < kFullSlots ? base + 1 : base + 2];
+            for (int it = 0; it < kIters; ++it) {
+                const int i = min(tid + it * NT, kPieces - 1);
+                const int j = i / (kRow / kVec);
+                const int q = i - j * (kRow / kVec);
+                const T *src = x + static_cast<int64_t>(min(b0 + j, M - 1)) * K +
+                               static_cast<int64_t>(g0) * kBlockWeights + q * kVec;
+                v[it] = *reinterpret_cast<const uint4 *>(src);
+            }
+        } else {
+#pragma unroll
+            for (int it = 0; it < kElemIters; ++it) {
+                const int i = min(tid + it * NT, BT * kRow - 1);
+                const int j = i / kRow;
+                e[it] = x[static_cast<int64_t>(min(b0 + j, M - 1)) * K + static_cast<int64_t>(g0) * kBlockWeights +
+                          (i - j * kRow)];
+            }
+        }
     }
-}
-
-// Uses every loaded activation in an empty asm statement placed after the
-// wait for them: none of the loads can then be sunk behind later ones (the
-// compiler would otherwise move the third activation of a task into the table
-// build's L3 branch, behind the word loads).
-template <typename T, int N>
-__device__ __forceinline__ void pin_loaded(const T (&xv)[N][3]) {
-    using Bits = std::conditional_t<sizeof(T) == 2, uint16_t, uint32_t>;
+    __device__ __forceinline__ void store(T (*xs)[kRow], int tid) const {
+        if (aligned) {
 #pragma unroll
-    for (int it = 0; it < N; ++it)
+            for (int it = 0; it < kIters; ++it) {
+                const int i = min(tid + it * NT, kPieces - 1);
+                const int j = i / (kRow / kVec);
+                *reinterpret_cast<uint4 *>(&xs[j][(i - j * (kRow / kVec)) * kVec]) = v[it];
+            }
+        } else {
 #pragma unroll
-        for (int k = 0; k < 3; ++k) asm volatile("" ::"v"(__builtin_bit_cast(Bits, xv[it][k])));
-}
-
-// Table task k of one group (k < 25: L2 slot k from x[5k], x[5k+1]; k < 50:
-// L3 slot k - 25 from x[5s+2..5s+4]; k = 50: the tail from x[125..127]), the
-// activations x0..x2 raw. Entries are (t - 1) * x as real products, so
-// 0 * inf = NaN propagates as in the reference.
-template <typename T>
-__device__ __forceinline__ void write_lut_task(float *L, int k, T xr0, T xr1, T xr2) {
-    const float x0 = to_f32<T>(xr0);
-    const float x1 = to_f32<T>(xr1);
-    const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
-    const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
-    if (k < kFullSlots) {
-        float *dst = L + k * kL2Entries;
-#pragma unroll
-        for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
-    } else {
-        const float x2 = to_f32<T>(xr2);
-        const float d[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
-        const int s = k - kFullSlots;
-        float *dst = L + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
-#pragma unroll
-        for (int e = 0; e < kL3Entries; ++e) dst[e] = (a[e % 3] + b[(e / 3) % 3]) + d[e / 9];
+            for (int it = 0; it < kElemIters; ++it) {
+                const int i = min(tid + it * NT, BT * kRow - 1);
+                const int j = i / kRow;
+                xs[j][i - j * kRow] = e[it];
+            }
+        }
     }
-}
+};
 
+// The LUT23 tables of one sub-chunk from its staged activations. Per
+// (vector, group): 25 L2 tasks (slot s: 9 entries from x[5s], x[5s+1]), and
+// 26 three-trit tasks (L3 slot s: 27 entries from x[5s+2..5s+4]; the tail:
+// 27 from x[125..127]). The three-trit tasks take threads [0, T3) and the L2
+// tasks start at the next multiple of 64, so every wave runs one kind of
+// task. A three-trit table is built from its 9 two-trit sums,
+// entry e = pair[e % 9] + d[e / 9] -- the reference's (a + b) + d, rounded
+// the same way. Entries are (t - 1) * x as real products, so 0 * inf = NaN
+// propagates as in the reference.
 template <typename T, int C, int BT, int NT>
-__device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats],
-                                                 const T (&xv)[lut_task_iters(C, BT, NT)][3], int tid) {
+__device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats], const T (*xs)[C * kBlockWeights],
+                                                 int tid) {
+    constexpr int kTrit3 = BT * C * (kFullSlots + 1);
+    constexpr int kL2Start = (kTrit3 + 63) / 64 * 64;
+    constexpr int kTasks = kL2Start + BT * C * kFullSlots;
 #pragma unroll
-    for (int it = 0; it < lut_task_iters(C, BT, NT); ++it) {
-        // A clamped (repeated) task writes the same values to the same entries.
-        const int task = min(tid + it * NT, lut_task_count(C, BT) - 1);
-        const int j = task / (C * kTasksPerGroup);
-        const int rem = task - j * (C * kTasksPerGroup);
-        const int c = rem / kTasksPerGroup;
-        const int k = rem - c * kTasksPerGroup;
-        write_lut_task<T>(lut[j][c], k, xv[it][0], xv[it][1], xv[it][2]);
+    for (int it = 0; it < (kTasks + NT - 1) / NT; ++it) {
+        const int i = tid + it * NT;
+        if (i < kTrit3) {
+            const int j = i / (C * (kFullSlots + 1));
+            const int rem = i - j * (C * (kFullSlots + 1));
+            const int c = rem / (kFullSlots + 1);
+            const int s = rem - c * (kFullSlots + 1);
+            const T *xg = xs[j] + c * kBlockWeights + (s < kFullSlots ? 5 * s + 2 : 125);
+            const float x0 = to_f32<T>(xg[0]), x1 = to_f32<T>(xg[1]), x2 = to_f32<T>(xg[2]);
+            const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
+            const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
+            const float d[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
+            float pair[kL2Entries];
+#pragma unroll
+            for (int e = 0; e < kL2Entries; ++e) pair[e] = a[e % 3] + b[e / 3];
+            float *dst = lut[j][c] + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
+#pragma unroll
+            for (int e = 0; e < kL3Entries; ++e) dst[e] = pair[e % 9] + d[e / 9];
+        } else if (i >= kL2Start && i < kTasks) {
+            const int t = i - kL2Start;
+            const int j = t / (C * kFullSlots);
+            const int rem = t - j * (C * kFullSlots);
+            const int c = rem / kFullSlots;
+            const int s = rem - c * kFullSlots;
+            const T *xg = xs[j] + c * kBlockWeights + 5 * s;
+            const float x0 = to_f32<T>(xg[0]), x1 = to_f32<T>(xg[1]);
+            const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
+            const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
+            float *dst = lut[j][c] + s * kL2Entries;
+#pragma unroll
+            for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
+        }
     }
 }
 
@@ -689,6 +724,7 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     constexpr int NT = kThreads * KW;
     constexpr int CB = C / KW;
     __shared__ float lut[BT][C][kLutFloats];
+    __shared__ __align__(16) T xs[BT][C * kBlockWeights];
     __shared__ float2 xchg[KW > 1 ? (KW - 1) * CB * BT : 1][kThreads];
     __shared__ unsigned s_last;
 
@@ -710,6 +746,7 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * KW * (kThreads / 64) + (tid >> 6);
     (void)lut_wave_id;
     TQ1_PHASE(lut_wave_id, 0);  // wave start
+    TQ1_PHASE_XCC(lut_wave_id);
 
     float acc[BT];
 #pragma unroll
@@ -731,14 +768,13 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     //      then one fma with the scale; blocks fold into acc in order -- the
     //      reference's summation order. Streams above 0 leave their block sums
     //      and scales in LDS; stream 0 folds them after a barrier.
-    using XV = T[lut_task_iters(C, BT, NT)][3];
     const int cb0 = stream * CB;  // first block of this wave's stream
     const char *const lut_bytes = reinterpret_cast<const char *>(&lut[0][0][0]);
     const uint32_t lut_base = static_cast<uint32_t>(cb0 * kLutFloats * 4);
     auto table = [&](uint32_t address, int j, int c, int entry) {
         return *reinterpret_cast<const float *>(lut_bytes + address + ((j * C + c) * kLutFloats + entry) * 4);
     };
-    auto run = [&](const XV &xv, int g0) {
+    auto run = [&](int g0) {
         const uint32_t *wp = row_words + (static_cast<int64_t>(g0) * kBlockWords + cb0 * kBlockWords) * kTileRows;
         uint32_t w[CB][kBlockWords];
 #pragma unroll
@@ -746,13 +782,14 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
 #pragma unroll
             for (int j = 0; j < kBlockWords; ++j) w[c][j] = wp[(c * kBlockWords + j) * kTileRows];
         __builtin_amdgcn_sched_barrier(0);
+        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 2);  // first words issued
         // (With several streams the fold barrier below already orders the
         // previous sub-chunk's table and exchange reads before this.)
         if (KW == 1 && g0 != g_begin) __syncthreads();
-        build_lut_tables<T, C, BT, NT>(lut, xv, tid);
-        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 1);  // own table entries written
+        build_lut_tables<T, C, BT, NT>(lut, xs, tid);
+        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 3);  // own table entries written
         __syncthreads();
-        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 2);  // tables ready
+        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 4);  // tables ready
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
             if (c + kLutLoadAhead < CB) {
@@ -807,17 +844,21 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         }
     };
     for (int g0 = g_begin; g0 < g_end; g0 += C) {
-        // Activations first, waited for before any word is issued: behind the
-        // chip-wide burst of word loads an activation load takes longer than
-        // the wait (measured gate/up 9.84 -> 9.70 us, QKV 8.01 -> 7.82).
-        XV xv;
-        load_lut_inputs<T, C, BT, NT>(xv, x, K, M, b0, g0, tid);
-        wait_vector_memory();
-        pin_loaded(xv);
-        run(xv, g0);
+        // Activations first, copied to LDS and waited for before any word is
+        // issued. Their lines are first read from HBM, where the chip-wide
+        // burst of word loads would queue ahead of them: issued just ahead
+        // of the words (no wait), the first waves of an XCC had them at
+        // 0.9 us instead of 0.5 (gate/up 9.28 -> 9.87 us on MI355X); read
+        // with scalar loads, 2.1 us.
+        ActivationCopy<T, C, BT, NT> copy;
+        copy.issue(x, K, M, b0, g0, tid);
+        copy.store(xs, tid);
+        if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 1);  // own activation copies arrived
+        __syncthreads();
+        run(g0);
     }
 
-    TQ1_PHASE(lut_wave_id, 3);  // all blocks summed
+    TQ1_PHASE(lut_wave_id, 5);  // all blocks summed
     // 4. Output. With GLU, rows 2r and 2r+1 are the gate and up rows of one
     // SwiGLU unit and sit in adjacent lanes: each lane rounds its value as the
     // unfused linear would, the even lane takes its partner's and writes
@@ -860,14 +901,14 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     asm volatile("" ::: "memory");
     wait_vector_memory();
     asm volatile("" ::: "memory");
-    TQ1_PHASE(lut_wave_id, 4);  // partial stored and acknowledged
+    TQ1_PHASE(lut_wave_id, 6);  // partial stored and acknowledged
     __syncthreads();
     unsigned *counter = counters + static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
     if (tid == 0)
         s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  static_cast<unsigned>(k_split - 1);
     __syncthreads();
-    TQ1_PHASE(lut_wave_id, 5);  // arrival counted
+    TQ1_PHASE(lut_wave_id, 7);  // arrival counted
     if (!s_last) return;
     const int64_t stride = static_cast<int64_t>(M) * N;
 #pragma unroll
@@ -876,7 +917,7 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
         store(j, row_ok && b0 + j < M ? sum_partials_in_order(src, stride, k_split) : 0.0f);
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    TQ1_PHASE(lut_wave_id, 6);  // fix-up done
+    TQ1_PHASE(lut_wave_id, 8);  // fix-up done
 }
 
 // The elementwise SwiGLU step over a linear's output whose rows alternate
