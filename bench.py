@@ -63,6 +63,9 @@ def parse() -> argparse.Namespace:
                    help="load the phase-timestamp build of the engine and summarise where a cold M=1 GEMV "
                         "launch spends its time, per configs[1] matrix (one JSON line each), next to the "
                         "graph-timed stream GEMV and LUT23 kernel")
+    p.add_argument("--phase-batch", type=int, default=1,
+                   help="activation rows of the --phase-profile launches: 1 profiles the LUT23 GEMV, more the "
+                        "kernel the library's dispatch picks for that batch (stamped: the direct-fragment form)")
     p.add_argument("--prefill-probe", action="store_true",
                    help="run only the M=512 prefill GEMMs (gate/up, down), 2 warm-up + --steps eager launches "
                         "each, for rocprofv3 --pmc MFMA-utilisation passes")
@@ -264,8 +267,8 @@ def main() -> int:
     if args.stream_ceiling:
         return stream_ceiling(torch, dev, graph_of, time_graph)
     if args.phase_profile:
-        return phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedTensorLayout,
-                             MatmulConfig, graph_of, time_graph)
+        return phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_linear_words,
+                             PackedTensorLayout, MatmulConfig, graph_of, time_graph, args.phase_batch)
 
     if args.prefill_probe:
         # Eager launches only (counter collection serialises dispatches).
@@ -474,11 +477,12 @@ PHASES = ("start", "activations arrived", "first words issued", "own tables writ
           "blocks summed", "partial stored and acknowledged", "arrival counted", "fix-up done")
 
 
-def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedTensorLayout, MatmulConfig,
-                  graph_of, time_graph) -> int:
+def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_linear_words, PackedTensorLayout,
+                  MatmulConfig, graph_of, time_graph, batch: int = 1) -> int:
     """Per configs[1] matrix: three cold launches of the M=1 GEMV (the LUT23
-    kernel) with the phase stamps of every wave (100 MHz wall clock, lane 0)
-    and the XCC it ran on. Wall clocks of different XCCs are not comparable,
+    kernel; with batch > 1 the kernel the library's dispatch picks, of which
+    the direct-fragment form is stamped) with the phase stamps of every wave
+    (100 MHz wall clock, lane 0) and the XCC it ran on. Wall clocks of different XCCs are not comparable,
     so every time is taken against the first wave start of the wave's own
     XCC: each phase's time, the XCC's span (first start to last stamp), each
     phase's duration per wave, and the time to the tables by the quarter of
@@ -507,14 +511,17 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedT
         lay = PackedTensorLayout.for_tensor(N, K)
         weights = [pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
                    for r in range(ring)]
-        x = synthetic.device_activations(1, K, seed=synthetic.SEED_BASE + 1 + i)
-        graph_ms = time_graph(graph_of(lambda: [tq1_matmul_words(weights[r % ring], x, layout=lay)
-                                                for r in range(ring * 4)])) / (ring * 4)
+        x = synthetic.device_activations(batch, K, seed=synthetic.SEED_BASE + 1 + i)
+
+        def gemv(w):
+            return tq1_matmul_words(w, x, layout=lay) if batch == 1 else tq1_linear_words(w, x, layout=lay)
+
+        graph_ms = time_graph(graph_of(lambda: [gemv(weights[r % ring]) for r in range(ring * 4)])) / (ring * 4)
         phase_times = {phase: [] for phase in PHASES}
         spans, durations, by_start = [], {}, [[] for _ in range(4)]
         for r in range(3):  # three cold launches, each over a copy last read 13 launches ago
             fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
-            tq1_matmul_words(weights[(r + 5) % ring], x, layout=lay)
+            gemv(weights[(r + 5) % ring])
             waves = fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
             stamps = [[buf[w * slots + p] for p in range(slots)] for w in range(waves)]
             stamps = [st for st in stamps if st[0] and st[slots - 1]]
@@ -530,11 +537,12 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, PackedT
                     part = ranked[q * quarter:(q + 1) * quarter] if q < 3 else ranked[3 * quarter:]
                     by_start[q] += [((st[0] - t0) / 100, (st[3] - st[0]) / 100, (st[1] - st[0]) / 100,
                                      (st[2] - st[1]) / 100) for st in part if st[3] and st[1] and st[2]]
-            for p in range(1, len(PHASES)):
-                durations.setdefault(f"{PHASES[p - 1]} -> {PHASES[p]}", []).extend(
-                    (st[p] - st[p - 1]) / 100 for st in stamps if st[p] and st[p - 1])
+            for st in stamps:  # between consecutive phases the wave stamped
+                present = [p for p in range(len(PHASES)) if st[p]]
+                for a, b in zip(present, present[1:]):
+                    durations.setdefault(f"{PHASES[a]} -> {PHASES[b]}", []).append((st[b] - st[a]) / 100)
         print(json.dumps({
-            "phase_profile": name, "K": K, "N": N, "waves_per_launch": len(phase_times["start"]) // 3,
+            "phase_profile": name, "K": K, "N": N, "M": batch, "waves_per_launch": len(phase_times["start"]) // 3,
             "gemv_graph_us": round(graph_ms * 1e3, 3),
             "xcc_span_us": quantiles(spans),
             "phases_after_xcc_first_wave_start": {ph: quantiles(v) for ph, v in phase_times.items() if v},

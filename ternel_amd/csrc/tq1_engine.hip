@@ -1252,8 +1252,11 @@ __device__ __forceinline__ void direct_mfma(float16v (&acc)[NB], const uint32_t 
 // direct_source_unit(u) of the group (the K order above).
 __device__ __forceinline__ int direct_source_unit(int u) { return u < 15 ? u : (u == 15 ? 30 : (u < 31 ? u - 1 : 31)); }
 
+// Three waves per SIMD for one activation tile: a CU then holds three
+// workgroups, so the grid (about 2.7 workgroups per CU at the 27B shapes)
+// runs in one round.
 template <int NB, int SR>
-__global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
+__global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_kernel(
     const uint32_t *__restrict__ packed, const _Float16 *__restrict__ x, _Float16 *__restrict__ y,
     float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
     int k_split, int window) {
@@ -1268,6 +1271,10 @@ __global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
     const int row0 = blockIdx.x * kDirectRows + wave * 32;
     const int g_begin = blockIdx.y * chunk_groups;
     const int cg = chunk_groups;
+    const int direct_wave_id = (blockIdx.y * gridDim.x + blockIdx.x) * kDirectWaves + wave;
+    (void)direct_wave_id;
+    TQ1_PHASE(direct_wave_id, 0);  // wave start
+    TQ1_PHASE_XCC(direct_wave_id);
     const int64_t K = static_cast<int64_t>(G) * kBlockWeights;
 
     // Rows past the padded last tile load the last padded row (discarded).
@@ -1275,11 +1282,8 @@ __global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
     const uint32_t *wrow = packed + static_cast<int64_t>(load_row / kTileRows) * G * kTileGroupWords + (load_row % kTileRows);
     const int wfirst = (upper ? 3 : 0) * kTileRows;
     const int wother = (upper ? 0 : 6) * kTileRows;
-
-    // LDS-DMA staging of one activation row per instruction: lane l fetches
-    // logical dword l of the row (physical unit direct_source_unit(l / 2)), the
-    // hardware writes it at row base + 4 l. Rows past M re-read row M - 1.
     const int src_half = direct_source_unit(lane >> 1) * 4 + (lane & 1) * 2;
+
     // B fragments: activation row (lane & 31) (+32 for the second tile); rows
     // past SR read row SR - 1 (their MFMA columns are never stored).
     const int brow = min(lane & 31, SR - 1);
@@ -1307,16 +1311,59 @@ __global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
         auto xb = [&](int q) { return xs + q * SR * kDirectStride + bofs; };
 
         if (w0) __syncthreads();  // every wave is done with the previous window's activations
+        // The window's activations, staged in LDS in the K order above
+        // (logical unit u of a row, 4 halves, from physical unit
+        // direct_source_unit(u); rows past M re-read row M - 1). Up to 16
+        // staged rows: as 8-byte units loaded into registers (16 per thread at
+        // the window of 8 groups) ahead of the first two word sets and written
+        // to LDS after them -- loads complete in order, so the writes wait for
+        // the activations only while the words are in flight. More rows: by
+        // LDS-DMA (one padded row per instruction) waited for before any word
+        // is requested, as a second register pass would wait for the words too.
+        // (Measured on MI355X, gate/up: M=16 20.7 -> 19.0 us and M=8 19.2 ->
+        // 18.3 us with registers, M=32 27.8 us with LDS-DMA against 32.4.)
         uint32_t wa[CH][5], wb[CH][5];
-        load_chunk(wa, 0);
-        load_chunk(wb, CH);
-        for (int r = wave; r < wn * SR; r += kDirectWaves) {
-            const int q = r / SR, m = r - q * SR;
-            const _Float16 *src = x + static_cast<int64_t>(min(m, M - 1)) * K + static_cast<int64_t>(gw + q) * kBlockWeights + src_half;
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
-                                             (__attribute__((address_space(3))) void *)(xs + r * kDirectStride), 4, 0, 0);
+        if constexpr (SR <= 16) {
+            constexpr int kUnits = 16;  // per thread
+            const int units = wn * SR * 32;
+            auto unit_source = [&](int i) {
+                const int r = i >> 5, q = r / SR, m = r - q * SR;
+                return reinterpret_cast<const uint2 *>(x + static_cast<int64_t>(min(m, M - 1)) * K +
+                                                       static_cast<int64_t>(gw + q) * kBlockWeights +
+                                                       direct_source_unit(i & 31) * 4);
+            };
+            auto unit_target = [&](int i) {
+                return reinterpret_cast<uint2 *>(xs + (i >> 5) * kDirectStride + (i & 31) * 4);
+            };
+            // Indices past the window are clamped (those threads load and write
+            // the last unit again, the same value): no load or write behind a
+            // branch, where the compiler's wait counts turn conservative.
+            const int first = min(units, kUnits * kDirectThreads);
+            uint2 xu[kUnits];
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) xu[k] = *unit_source(min(tid + k * kDirectThreads, first - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            load_chunk(wa, 0);
+            load_chunk(wb, CH);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < kUnits; ++k) *unit_target(min(tid + k * kDirectThreads, first - 1)) = xu[k];
+            // (Windows of more than 8 groups at 16 rows: the rest after the words.)
+            for (int i = first + tid; i < units; i += kDirectThreads) *unit_target(i) = *unit_source(i);
+        } else {
+            for (int r = wave; r < wn * SR; r += kDirectWaves) {
+                const int q = r / SR, m = r - q * SR;
+                const _Float16 *src = x + static_cast<int64_t>(min(m, M - 1)) * K +
+                                      static_cast<int64_t>(gw + q) * kBlockWeights + src_half;
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                                 (__attribute__((address_space(3))) void *)(xs + r * kDirectStride),
+                                                 4, 0, 0);
+            }
+            wait_vector_memory();
+            load_chunk(wa, 0);
+            load_chunk(wb, CH);
         }
-        wait_vector_memory();
+        if (w0 == 0) TQ1_PHASE(direct_wave_id, 1);  // first window's activations staged
         __syncthreads();
 
         // Pipeline over the window (no barriers): MFMAs of group q interleaved
@@ -1362,45 +1409,67 @@ __global__ __launch_bounds__(kDirectThreads) void direct_gemm_kernel(
         }
     }
 
+    TQ1_PHASE(direct_wave_id, 5);  // every group summed
     // D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) % 2), item 4 * (i / 8) + i % 4;
     // here i is a weight row of the wave and j an activation row.
     if (k_split > 1) {
-        // Partials in fragment order (coalesced, each lane re-reads its own).
-        constexpr int kFrag = NB * 16 * 64;
-        float *mine = partial + ((static_cast<int64_t>(blockIdx.x) * k_split + blockIdx.y) * kDirectWaves + wave) * kFrag + lane;
+        // Partials in fragment order, only the lanes of real activation rows:
+        // item r of tile nb in lane j + 32 h goes to ((nb * 16 + r) * 2 + h) * S
+        // + j with S = min(M, 32), so a batch of 8 writes a quarter of the 32
+        // columns an MFMA tile holds (each lane re-reads its own).
+        const int S = min(M, 32);
+        const int frag = NB * 32 * S;
+        const int j = lane & 31;
+        const int slot = (lane >> 5) * S + j;
+        float *mine = partial + ((static_cast<int64_t>(blockIdx.x) * k_split + blockIdx.y) * kDirectWaves + wave) * frag + slot;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
+            if (nb * 32 + j < M)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                __hip_atomic_store(mine + (nb * 16 + r) * 64, acc[nb][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int r = 0; r < 16; ++r)
+                    __hip_atomic_store(mine + (nb * 16 + r) * 2 * S, acc[nb][r], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         wait_vector_memory();
+        TQ1_PHASE(direct_wave_id, 6);  // partial stored and acknowledged
         __syncthreads();
         unsigned *counter = counters + blockIdx.x;
         if (tid == 0)
             s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                      static_cast<unsigned>(k_split - 1);
         __syncthreads();
+        TQ1_PHASE(direct_wave_id, 7);  // arrival counted
         if (!s_last) return;
-        const float *base = partial + (static_cast<int64_t>(blockIdx.x) * k_split * kDirectWaves + wave) * kFrag + lane;
-        const int64_t chunk_stride = static_cast<int64_t>(kDirectWaves) * kFrag;
+        const float *base = partial + (static_cast<int64_t>(blockIdx.x) * k_split * kDirectWaves + wave) * frag + slot;
+        const int64_t chunk_stride = static_cast<int64_t>(kDirectWaves) * frag;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
-        for (int z = 0; z < k_split; ++z) {
-            float v[NB][16];
+        // The chunks are added in chunk order, kBatch of them per memory
+        // round trip (all their loads issued before the first add; a batch
+        // past the last chunk re-reads it and adds nothing).
+        constexpr int kBatch = NB == 1 ? 8 : 4;
+        for (int z0 = 0; z0 < k_split; z0 += kBatch) {
+            float v[kBatch][NB][16];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+            for (int u = 0; u < kBatch; ++u)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    v[nb][r] = __hip_atomic_load(base + z * chunk_stride + (nb * 16 + r) * 64, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+                for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+                    for (int r = 0; r < 16; ++r)
+                        v[u][nb][r] = __hip_atomic_load(base + min(z0 + u, k_split - 1) * chunk_stride +
+                                                            (nb * 16 + r) * 2 * S,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[nb][r] += v[nb][r];
+            for (int u = 0; u < kBatch; ++u)
+                if (z0 + u < k_split)
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[nb][r] += v[u][nb][r];
         }
         if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        TQ1_PHASE(direct_wave_id, 8);  // fix-up sums done
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -2394,8 +2463,9 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
         window -= window % 8;
     plan->window = window;
     plan->lds_bytes = static_cast<size_t>(window) * group_bytes;
-    plan->partial_bytes = k_split > 1 ? static_cast<size_t>(k_split) * plan->row_blocks * kDirectRows * 32 *
-                                            plan->nb * sizeof(float)
+    // Partials of the real activation columns only (at most 32 per tile).
+    plan->partial_bytes = k_split > 1 ? static_cast<size_t>(k_split) * plan->row_blocks * kDirectRows *
+                                            std::min<int64_t>(M, 32) * plan->nb * sizeof(float)
                                       : 0;
     return TERNEL_TQ1_OK;
 }

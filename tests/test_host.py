@@ -244,7 +244,8 @@ def test_workspace_queries() -> None:
     assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, 0, 2) == counters + 2 * 512 * 17408 * 4
     # direct form: partials are 128 rows x 32 (or 64) activation columns per row block and chunk
     assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, direct, 1) == 0
-    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, direct, 5) == counters + 5 * 2 * 128 * 32 * 4
+    # partials of the 8 real activation columns only
+    assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, direct, 5) == counters + 5 * 2 * 128 * 8 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(40, 300, 5120, direct, 4) == counters + 4 * 3 * 128 * 64 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(65, 256, 5120, direct, 1) == 0  # rejected
     # wide form: two fp32 partial slots of 8 waves x NB fragments x 16 x 64 per
