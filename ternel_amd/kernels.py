@@ -249,7 +249,8 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
 def workspace_errors() -> dict[tuple[int, int], int]:
     """The error word of every workspace (synchronises each one's stream): a
     nonzero word names the kernels whose bounded wait for another workgroup's
-    partial gave up (1 = the M=1 stream GEMV, 2 = the wide GEMM)."""
+    partial gave up (2 = the wide GEMM's stream-K reduction; the LUT23 and
+    direct-form fix-ups never wait)."""
     handle = _lib.lib()
     words = {}
     for (index, stream), buf in _WORKSPACES.items():
