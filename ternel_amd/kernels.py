@@ -53,7 +53,7 @@ class MatmulConfig:
     ``batch_tile`` (1, 2 or 4 vectors per workgroup) and ``k_split`` (K chunks,
     dividing the groups per row, reduced in chunk order) are honoured; ``0``
     means automatic for both -- one vector per workgroup and the split measured
-    best for the shape, and at M = 1 the stream GEMV. ``threads``,
+    best for the shape. ``threads``,
     ``padded_lut`` and ``safe_clamp`` are the Metal kernel's own template knobs:
     they are validated as the reference validates them and otherwise have no
     effect (the gfx950 kernels fix their workgroup sizes, keep one table layout
@@ -275,8 +275,7 @@ def check_workspaces() -> None:
 
 def tq1_matmul_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
                      config: MatmulConfig | None = None) -> torch.Tensor:
-    """``x @ W.T`` through the LUT23 kernels (at M = 1 with automatic knobs the
-    stream GEMV); ``(batch, rows)`` in ``x.dtype``. A ``k_split`` that does not
+    """``x @ W.T`` through the LUT23 kernel; ``(batch, rows)`` in ``x.dtype``. A ``k_split`` that does not
     divide the group count is refused, as the reference refuses it
     (src/ternel_mlx/kernels.py:1240-1246)."""
     config = config or MatmulConfig()
