@@ -45,6 +45,65 @@ __host__ __device__ __attribute__((always_inline)) inline V lut23_low(V p, V hig
     return p - high * static_cast<unsigned short>(9);
 }
 
+// The other split of a code byte, into its three low and two high digits:
+// high = (p * 19) >> 9, equal to p / 27 for every byte value, and low =
+// p - 27 * high (0..26). For every byte value high <= 9.
+template <typename V>
+__host__ __device__ __attribute__((always_inline)) inline V split27_high(V p) {
+    return (p * static_cast<unsigned short>(19)) >> static_cast<unsigned short>(9);
+}
+template <typename V>
+__host__ __device__ __attribute__((always_inline)) inline V split27_low(V p, V high) {
+    return p - high * static_cast<unsigned short>(27);
+}
+
+// Selector tables of the MFMA decoders. A weight with digit d is bytes
+// (2d, 2d + 1) of the 8-byte table {-s, z, +s, 0} that v_perm_b32 selects
+// from, so a dword of two weights' selectors turns into their fp16 pair with
+// one v_perm_b32. A pair of consecutive code bytes (a, b) gives its ten
+// weights as five pairs (digit i of a byte has weight 3^i):
+//   (a0, a1) = T9a[a % 9]
+//   (a2, a3) = T27aX[a / 9]
+//   (a4, b0) = T27aY[a / 9] | T27bX[b % 27]
+//   (b1, b2) = T27bY[b % 27]
+//   (b3, b4) = T9b[b / 27]
+// The tail byte t (three digits) reads as a b byte's low part: (t0 in the
+// high half) = T27bX[t], (t1, t2) = T27bY[t]. Each table is at most 29 dwords, so a
+// wave's lookups into one never conflict in the LDS banks. Indices of illegal
+// bytes (a / 9 up to 28, b / 27 up to 9) stay inside their tables; their
+// entries select bytes 6-7 of the table, a zero.
+constexpr int kSelT9a = 0;     // 9 entries: l = a0 + 3 a1
+constexpr int kSelT27aX = 9;   // 29 entries: h = a2 + 3 a3 + 9 a4
+constexpr int kSelT27aY = 38;  // 29 entries, the same index: a4 in the low half
+constexpr int kSelT27bX = 67;  // 27 entries: m = b0 + 3 b1 + 9 b2: b0 in the high half
+constexpr int kSelT27bY = 94;  // 27 entries, the same index: (b1, b2)
+constexpr int kSelT9b = 121;   // 10 entries: n = b3 + 3 b4
+constexpr int kSelEntries = 131;
+
+__host__ __device__ __attribute__((always_inline)) inline uint32_t selector_half(uint32_t d) {
+    return (2u * d) | ((2u * d + 1u) << 8);
+}
+__host__ __device__ __attribute__((always_inline)) inline uint32_t selector_pair(uint32_t d_even, uint32_t d_odd) {
+    return selector_half(d_even) | (selector_half(d_odd) << 16);
+}
+
+// Entry i of the concatenated selector tables.
+__host__ __device__ inline uint32_t selector_entry(int i) {
+    if (i < kSelT27aX) return selector_pair(i % 3, i / 3);
+    if (i < kSelT27aY) {
+        const int h = i - kSelT27aX;
+        return selector_pair(h % 3, (h / 3) % 3);
+    }
+    if (i < kSelT27bX) return selector_half((i - kSelT27aY) / 9);
+    if (i < kSelT27bY) return selector_half((i - kSelT27bX) % 3) << 16;
+    if (i < kSelT9b) {
+        const int m = i - kSelT27bY;
+        return selector_pair((m / 3) % 3, m / 9);
+    }
+    const int n = i - kSelT9b;
+    return selector_pair(n % 3, n / 3);
+}
+
 // Tail-table entry of a tail byte: the byte itself, clamped to the table.
 __host__ __device__ __attribute__((always_inline)) inline uint32_t tail_entry(uint32_t p) {
     return p < kMaxTailByte ? p : kMaxTailByte;

@@ -1177,48 +1177,79 @@ constexpr int kDirectLdsBytes = 160 * 1024 - 1024;      // dynamic LDS budget (g
 constexpr int kDirectStride = kBlockWeights + 8;      // halves per staged activation row
 
 
+// The 32 selector dwords of one half block (pairs of weights, in the direct K
+// order), from the selector tables in LDS (sel_bytes, tq1_bytes.h): u[0..3]
+// hold the half's twelve code bytes at bytes 2..13, w6 code byte 24 (byte 2)
+// and the tail byte (byte 3). Code bytes 2w, 2w+1 give pairs 5w .. 5w+4;
+// pairs 30 and 31 are code byte 24's first four weights in the lower half
+// and, in the upper half, its fifth with the three tail weights.
+__device__ __forceinline__ void half_block_selectors(const uint32_t (&u)[4], uint32_t w6, bool upper,
+                                                     const char *sel_bytes, uint32_t (&sel)[32]) {
+    auto lds = [&](uint32_t address, int entry) {
+        return *reinterpret_cast<const uint32_t *>(sel_bytes + address + entry * 4);
+    };
+    const uint32_t zero = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        // the a bytes (even code bytes) of windows 2k, 2k+1 and their b bytes,
+        // one per 16-bit half
+        const u16x2 a = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(u[k + 1], u[k], 0x0c040c02u));
+        const u16x2 b = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(u[k + 1], u[k], 0x0c050c03u));
+        const u16x2 ha = tq1_bytes::lut23_high(a), la = tq1_bytes::lut23_low(a, ha);
+        const u16x2 hb = tq1_bytes::split27_high(b), lb = tq1_bytes::split27_low(b, hb);
+        const uint32_t la2 = __builtin_bit_cast(uint32_t, la), ha2 = __builtin_bit_cast(uint32_t, ha);
+        const uint32_t lb2 = __builtin_bit_cast(uint32_t, lb), hb2 = __builtin_bit_cast(uint32_t, hb);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int w = 2 * k + e;
+            const uint32_t al = e ? lut_address_hi(la2, zero) : lut_address_lo(la2, zero);
+            const uint32_t ah = e ? lut_address_hi(ha2, zero) : lut_address_lo(ha2, zero);
+            const uint32_t bl = e ? lut_address_hi(lb2, zero) : lut_address_lo(lb2, zero);
+            const uint32_t bh = e ? lut_address_hi(hb2, zero) : lut_address_lo(hb2, zero);
+            sel[5 * w] = lds(al, tq1_bytes::kSelT9a);
+            sel[5 * w + 1] = lds(ah, tq1_bytes::kSelT27aX);
+            sel[5 * w + 2] = lds(ah, tq1_bytes::kSelT27aY) | lds(bl, tq1_bytes::kSelT27bX);
+            sel[5 * w + 3] = lds(bl, tq1_bytes::kSelT27bY);
+            sel[5 * w + 4] = lds(bh, tq1_bytes::kSelT9b);
+        }
+    }
+    // (The half-dependent choices as bit blends with a lane mask: written as
+    // selects, they became an exec-masked branch.)
+    const uint32_t mask = 0u - static_cast<uint32_t>(upper);
+    auto blend = [&](uint32_t if_upper, uint32_t if_lower) { return (if_upper & mask) | (if_lower & ~mask); };
+    const uint32_t p24 = (w6 >> 16) & 0xffu;
+    const uint32_t t = tq1_bytes::tail_entry(w6 >> 24);
+    const uint32_t h24 = (p24 * 57u) >> 9, l24 = p24 - 9u * h24;
+    const uint32_t lead = lds(blend(4 * (t + tq1_bytes::kSelT27bX), 4 * (l24 + tq1_bytes::kSelT9a)), 0);
+    const uint32_t rest = lds(blend(4 * (t + tq1_bytes::kSelT27bY), 4 * (h24 + tq1_bytes::kSelT27aX)), 0);
+    const uint32_t fifth = lds(4 * h24, tq1_bytes::kSelT27aY);
+    sel[30] = lead | (fifth & mask);
+    sel[31] = rest;
+}
+
 // One pipeline step of direct_gemm_kernel: the MFMAs of the current group
 // (weights already decoded in a_mfma, activations in LDS buffer `buf`) with the
-// decode of the next group (words u, other -> a_dec) interleaved stage by
-// stage: decode stage st produces exactly the four dwords MFMA step st of the
-// following group will need.
+// decode of the next group (words u, other -> a_dec): its 32 selector dwords
+// from the tables in LDS up front, then at stage st the four weight pairs MFMA
+// step st of the following group will need.
 template <int NB, bool kMfma = true>
 __device__ __forceinline__ void direct_step(float16v (&acc)[NB], const uint32_t (&a_mfma)[32], uint32_t (&a_dec)[32],
                                             const uint32_t (&u)[4], uint32_t other, bool upper,
-                                            const _Float16 *xb, uint32_t scale_mask = 0xffffu) {
+                                            const _Float16 *xb, const char *sel_bytes,
+                                            uint32_t scale_mask = 0xffffu) {
     // scale_mask 0 turns a padding group's weights into +-0.
     uint32_t table_hi, table_lo;
     scale_tables((upper ? other : u[0]) & scale_mask, table_hi, table_lo);
-    uint32_t c[64];
+    uint32_t sel[32];
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
         half8 bf[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
             bf[nb] = *reinterpret_cast<const half8 *>(xb + nb * 32 * kDirectStride + st * 8);
-        // Bytes whose first position falls in this stage.
+        if (st == 0) half_block_selectors(u, upper ? u[3] : other, upper, sel_bytes, sel);
 #pragma unroll
-        for (int j = 0; j < 12; ++j) {
-            if ((5 * j) / 8 != st) continue;
-            const int b = 2 + j;
-            uint32_t d[5];
-            byte_digit_carriers((u[b >> 2] >> (8 * (b & 3))) & 0xffu, d);
-#pragma unroll
-            for (int i = 0; i < 5; ++i) c[5 * j + i] = d[i];
-        }
-        if (st == 7) {
-            const uint32_t w6 = upper ? u[3] : other;
-            uint32_t d24[5];
-            byte_digit_carriers((w6 >> 16) & 0xffu, d24);
-            uint32_t dt[3];
-            tail_digit_carriers(w6 >> 24, dt);
-            c[60] = upper ? d24[4] : d24[0];
-            c[61] = upper ? dt[0] : d24[1];
-            c[62] = upper ? dt[1] : d24[2];
-            c[63] = upper ? dt[2] : d24[3];
-        }
-#pragma unroll
-        for (int p = 4 * st; p < 4 * st + 4; ++p) a_dec[p] = weight_pair(c[2 * p], c[2 * p + 1], table_hi, table_lo);
+        for (int p = 4 * st; p < 4 * st + 4; ++p) a_dec[p] = __builtin_amdgcn_perm(table_hi, table_lo, sel[p]);
         if (!kMfma) continue;
         half8 af;
         {
@@ -1263,8 +1294,11 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
     static_assert(SR <= 32 * NB && SR >= 8, "staged rows");
     extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // window x SR rows x kDirectStride halves
     __shared__ unsigned s_last;
+    __shared__ uint32_t selectors[tq1_bytes::kSelEntries];
 
     const int tid = threadIdx.x;
+    if (tid < tq1_bytes::kSelEntries) selectors[tid] = tq1_bytes::selector_entry(tid);  // read after the first barrier
+    const char *const sel_bytes = reinterpret_cast<const char *>(selectors);
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
     const bool upper = lane >= 32;
@@ -1374,11 +1408,11 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
         uint32_t a0[32], a1[32];
         {
             const uint32_t u[4] = {wa[0][0], wa[0][1], wa[0][2], wa[0][3]};
-            direct_step<NB, false>(acc, a1, a0, u, wa[0][4], upper, xb(0));
+            direct_step<NB, false>(acc, a1, a0, u, wa[0][4], upper, xb(0), sel_bytes);
         }
         auto step = [&](const uint32_t (&a_mfma)[32], uint32_t (&a_dec)[32], const uint32_t (&w)[5], int q) {
             const uint32_t u[4] = {w[0], w[1], w[2], w[3]};
-            direct_step<NB>(acc, a_mfma, a_dec, u, w[4], upper, xb(q));
+            direct_step<NB>(acc, a_mfma, a_dec, u, w[4], upper, xb(q), sel_bytes);
         };
         int q = 0;
         for (; q + 2 * CH <= wn; q += 2 * CH) {
@@ -1404,7 +1438,7 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
             if (q + 1 < wn) {
                 const uint32_t *p = wrow + static_cast<int64_t>(gw + q + 1) * kTileGroupWords;
                 const uint32_t u[4] = {p[wfirst], p[wfirst + kTileRows], p[wfirst + 2 * kTileRows], p[wfirst + 3 * kTileRows]};
-                direct_step<NB, false>(acc, a1, a0, u, p[wother], upper, xb(q + 1));
+                direct_step<NB, false>(acc, a1, a0, u, p[wother], upper, xb(q + 1), sel_bytes);
             }
         }
     }

@@ -87,6 +87,62 @@ int main() {
     printf("digit carriers: 256 code and 256 tail bytes; every carrier's top byte is a digit in 0..2 (a v_perm_b32 "
            "selector pair 2d, 2d+1 <= 5 picks a scale-table byte); legal bytes exact\n");
 
+    // The selector tables of the MFMA decoders.
+    unsigned max_high27 = 0;
+    for (unsigned p = 0; p < 256; ++p) {
+        const unsigned short a = static_cast<unsigned short>(p);
+        const unsigned short h9 = lut23_high(a), l9 = lut23_low(a, h9);
+        const unsigned short h27 = split27_high(a), l27 = split27_low(a, h27);
+        max_high27 = h27 > max_high27 ? h27 : max_high27;
+        expect(h27 == p / 27 && l27 == p % 27, "split27 is p / 27, p % 27 for every byte value", p);
+        expect(kSelT9a + l9 < kSelT27aX, "T9a index inside T9a", p);
+        expect(kSelT27aX + h9 < kSelT27aY && kSelT27aY + h9 < kSelT27bX, "T27a index inside T27aX, T27aY", p);
+        expect(kSelT27bX + l27 < kSelT27bY && kSelT27bY + l27 < kSelT9b, "T27b index inside T27bX, T27bY", p);
+        expect(kSelT9b + h27 < kSelEntries, "T9b index inside T9b", p);
+        const unsigned t = tail_entry(p);
+        expect(kSelT27bX + t < kSelT27bY && kSelT27bY + t < kSelT9b, "tail index inside T27bX, T27bY", p);
+    }
+    for (unsigned a = 0; a < 256; ++a)
+        for (unsigned b = 0; b < 256; ++b) {
+            const u16x2 pair = {static_cast<unsigned short>(a), static_cast<unsigned short>(b)};
+            const u16x2 high = split27_high(pair);
+            const u16x2 low = split27_low(pair, high);
+            expect(high[0] == a / 27 && high[1] == b / 27 && low[0] == a % 27 && low[1] == b % 27,
+                   "packed split27 equals the per-byte split", a, b);
+        }
+    for (unsigned a = 0; a <= kMaxCodeByte; ++a)
+        for (unsigned b = 0; b <= kMaxCodeByte; ++b) {
+            const unsigned la = a % 9, ha = a / 9, lb = b % 27, hb = b / 27;
+            const uint32_t got[5] = {selector_entry(kSelT9a + la), selector_entry(kSelT27aX + ha),
+                                     selector_entry(kSelT27aY + ha) | selector_entry(kSelT27bX + lb),
+                                     selector_entry(kSelT27bY + lb), selector_entry(kSelT9b + hb)};
+            unsigned d[10];
+            for (int i = 0; i < 5; ++i) {
+                d[i] = digit(a, i);
+                d[5 + i] = digit(b, i);
+            }
+            for (int q = 0; q < 5; ++q)
+                expect(got[q] == selector_pair(d[2 * q], d[2 * q + 1]), "byte pair's selectors are its digits' pairs", a,
+                       static_cast<int>(b * 8 + q));
+        }
+    for (unsigned p = 0; p <= kMaxCodeByte; ++p)
+        for (unsigned t = 0; t <= kMaxTailByte; ++t) {
+            // code byte 24's fifth digit with the tail's first; the tail's last two
+            const uint32_t lead = selector_entry(kSelT27aY + p / 9) | selector_entry(kSelT27bX + tail_entry(t));
+            const uint32_t rest = selector_entry(kSelT27bY + tail_entry(t));
+            expect(lead == selector_pair(digit(p, 4), digit(t, 0)), "byte 24 and tail lead pair", p, t);
+            expect(rest == selector_pair(digit(t, 1), digit(t, 2)), "tail rest pair", p, t);
+        }
+    for (int i = 0; i < kSelEntries; ++i)
+        for (int k = 0; k < 4; ++k)
+            expect(((selector_entry(i) >> (8 * k)) & 0xffu) <= 7, "selector bytes pick inside the 8-byte table", i, k);
+    const int table_sizes[6] = {kSelT27aX - kSelT9a, kSelT27aY - kSelT27aX, kSelT27bX - kSelT27aY,
+                                kSelT27bY - kSelT27bX, kSelT9b - kSelT27bY, kSelEntries - kSelT9b};
+    for (int i = 0; i < 6; ++i) expect(table_sizes[i] <= 32, "each selector table within 32 banks", i);
+    printf("selector tables: %d entries; split27 high <= %u; every byte pair (a, b) <= 242 gives its ten digits' "
+           "selector pairs, byte 24 with every tail byte too; every index of all 256 byte values inside its table\n",
+           kSelEntries, max_high27);
+
     // The gather's per-byte digit table.
     for (unsigned b = 0; b < 256; ++b) {
         const uint32_t d = byte_digits(b);
