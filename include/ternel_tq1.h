@@ -255,7 +255,7 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
  * z is [M][rows / 2] in the activation type. No counterpart in the reference
  * (its MLP runs gate_proj, up_proj and the activation as separate mlx ops,
  * src/ternel_mlx/packed_model.py:72-92). Batches that ternel_tq1_linear sends
- * to the LUT23 kernel (up to 4 rows, 6 for matrices under 16 MiB, and every
+ * to the LUT23 kernel (up to 3 rows, 5 for matrices under 16 MiB, and every
  * bf16/fp32 batch) run it with the pair exchange in its epilogue; larger fp16
  * batches run the GEMM into the workspace and one elementwise pass. Workspace
  * from ternel_tq1_swiglu_workspace_bytes, same contract as ternel_tq1_linear's.

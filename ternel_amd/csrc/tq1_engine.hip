@@ -2657,15 +2657,21 @@ int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_
     const int64_t tiles_n = ceil_div(rows, kWideRows);
     const int nb = wide_blocks(M, tiles_n, groups, cus);
     const int64_t tiles = tiles_n * ceil_div(M, 32 * nb);
-    return 4 * tiles >= cus || tiles * groups >= 15 * cus ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_TILE;
+    // Measured on MI355X: at one or two activation blocks per tile 10 (tile,
+    // group) steps per CU suffice (down M=40-64: 38.5-39.7 us against the tile
+    // form's 47.4-48.1); four or eight blocks need 15 (down M=96-128 stays on
+    // the tile form, 49.0-52.0 us against 55.5-58.5).
+    const int64_t min_steps = nb <= 2 ? 10 : 15;
+    return 4 * tiles >= cus || tiles * groups >= min_steps * cus ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_TILE;
 }
 
 // The dispatch rule of packed_matmul, retuned for MI355X by the same sweep: the
-// LUT23 kernel up to 4 activation rows -- 6 for matrices under 16 MiB of
+// LUT23 kernel up to 3 activation rows -- 5 for matrices under 16 MiB of
 // packed weights, where the MFMA forms' fixed costs weigh more (O 8192->5120
-// M=5: 13.9 us against 16.6) -- the MFMA kernels above it (fp16 only).
-constexpr int64_t kLinearLutMaxBatch = 4;
-constexpr int64_t kLinearLutMaxBatchSmall = 6;
+// M=5: 13.6 us against 14.3; gate/up M=4: the direct form 17.9 us against
+// 19.3) -- the MFMA kernels above it (fp16 only).
+constexpr int64_t kLinearLutMaxBatch = 3;
+constexpr int64_t kLinearLutMaxBatchSmall = 5;
 constexpr int64_t kLinearSmallMatrixBytes = 16ll << 20;
 bool linear_uses_lut(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (dtype != TERNEL_TQ1_F16) return true;

@@ -275,9 +275,9 @@ def check_workspaces() -> None:
 
 def tq1_matmul_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTensorLayout,
                      config: MatmulConfig | None = None) -> torch.Tensor:
-    """``x @ W.T`` through the LUT23 kernel; ``(batch, rows)`` in ``x.dtype``. A ``k_split`` that does not
-    divide the group count is refused, as the reference refuses it
-    (src/ternel_mlx/kernels.py:1240-1246)."""
+    """``x @ W.T`` through the LUT23 kernel; ``(batch, rows)`` in ``x.dtype``.
+    A ``k_split`` that does not divide the group count is refused, as the
+    reference refuses it (src/ternel_mlx/kernels.py:1240-1246)."""
     config = config or MatmulConfig()
     check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)

@@ -19,7 +19,7 @@ import torch
 sys.path.insert(0, str(Path(__file__).resolve().parents[2]))
 
 from ternel_amd import synthetic  # noqa: E402
-from ternel_amd.kernels import GemmConfig, MatmulConfig, pack_weights, tq1_gemm, tq1_matmul  # noqa: E402
+from ternel_amd.kernels import GemmConfig, MatmulConfig, pack_weights, tq1_gemm_words, tq1_matmul_words  # noqa: E402
 from ternel_amd.layout import PackedTensorLayout  # noqa: E402
 
 SHAPES = (("gate_up", 5120, 17408), ("down", 17408, 5120), ("qkv", 5120, 8192), ("o", 8192, 5120))
@@ -54,11 +54,13 @@ def main(out: str) -> None:
             launches = max(4, min(2 * ring, 4096 // M))
             kernels = {}
             if M <= 64:
-                kernels["lut23"] = lambda i: tq1_matmul(weights[i % ring], x, layout=lay, config=MatmulConfig())
-                kernels["direct"] = lambda i: tq1_gemm(weights[i % ring], x, layout=lay,
-                                                       config=GemmConfig(form="direct"))
-            kernels["wide"] = lambda i: tq1_gemm(weights[i % ring], x, layout=lay, config=GemmConfig(form="wide"))
-            kernels["tile"] = lambda i: tq1_gemm(weights[i % ring], x, layout=lay, config=GemmConfig(form="tile"))
+                kernels["lut23"] = lambda i: tq1_matmul_words(weights[i % ring], x, layout=lay, config=MatmulConfig())
+                kernels["direct"] = lambda i: tq1_gemm_words(weights[i % ring], x, layout=lay,
+                                                             config=GemmConfig(form="direct"))
+            kernels["wide"] = lambda i: tq1_gemm_words(weights[i % ring], x, layout=lay,
+                                                       config=GemmConfig(form="wide"))
+            kernels["tile"] = lambda i: tq1_gemm_words(weights[i % ring], x, layout=lay,
+                                                       config=GemmConfig(form="tile"))
             times = {k: round(graph_us(fn, launches), 2) for k, fn in kernels.items()}
             rows.append({"shape": name, "K": K, "N": N, "M": M, "us": times})
             print(json.dumps(rows[-1]), flush=True)

@@ -86,7 +86,7 @@ def test_fused_swiglu_matches_the_unfused_layers(dtype, batch: int, hidden: int,
         bound = 1.01 * (dz_dg * dg + dz_du * du) + spacing(want.float(), dtype)
         assert bool((diff <= bound).all()), float((diff - bound).max())
     else:
-        # The LUT path (batches of 2 to 4, every bf16/fp32 batch) sums each row
+        # The LUT path (batches of 2 to 5 here, every bf16/fp32 batch) sums each row
         # in the same chunk order for the fused and the separate weights: gate
         # and up round to the same values and z agrees to SiLU's exp (an fp32
         # ulp against torch's) and one rounding step of z.
