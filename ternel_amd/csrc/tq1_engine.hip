@@ -1652,8 +1652,11 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     extern __shared__ __attribute__((aligned(16))) unsigned char wide_lds[];
     __shared__ unsigned s_last;
     __shared__ unsigned s_published;
+    __shared__ uint32_t selectors[tq1_bytes::kSelEntries];
 
     const int tid = threadIdx.x;
+    if (tid < tq1_bytes::kSelEntries) selectors[tid] = tq1_bytes::selector_entry(tid);  // read after the first barrier
+    const char *const sel_bytes = reinterpret_cast<const char *>(selectors);
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
     const bool upper = lane >= 32;
@@ -1759,7 +1762,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     // group's words w over them.
     auto step = [&](uint32_t (&a)[32], const uint32_t (&w)[5], int buf, bool mfma) {
         uint32_t th = 0, tl = 0;
-        uint32_t c[64];
+        uint32_t sel[32];
         const _Float16 *xb = reinterpret_cast<const _Float16 *>(xbuf0 + buf * kXBytes);
         auto frag = [&](int st, int nb) {
             return *reinterpret_cast<const half8 *>(xb + nb * 32 * kBlockWeights + frag_row + ((st ^ frag_l7) * 8));
@@ -1834,29 +1837,13 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                     if (st < 7) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
                 }
             }
-            if (st == 0) scale_tables((upper ? w[4] : w[0]) & 0xffffu, th, tl);
-#pragma unroll
-            for (int j = 0; j < 12; ++j) {
-                if ((5 * j) / 8 != st) continue;
-                const int bb = 2 + j;
-                uint32_t d[5];
-                byte_digit_carriers((w[bb >> 2] >> (8 * (bb & 3))) & 0xffu, d);
-#pragma unroll
-                for (int i = 0; i < 5; ++i) c[5 * j + i] = d[i];
-            }
-            if (st == 7) {
-                const uint32_t w6 = upper ? w[3] : w[4];
-                uint32_t d24[5];
-                byte_digit_carriers((w6 >> 16) & 0xffu, d24);
-                uint32_t dt[3];
-                tail_digit_carriers(w6 >> 24, dt);
-                c[60] = upper ? d24[4] : d24[0];
-                c[61] = upper ? dt[0] : d24[1];
-                c[62] = upper ? dt[1] : d24[2];
-                c[63] = upper ? dt[2] : d24[3];
+            if (st == 0) {
+                scale_tables((upper ? w[4] : w[0]) & 0xffffu, th, tl);
+                const uint32_t u[4] = {w[0], w[1], w[2], w[3]};
+                half_block_selectors(u, upper ? w[3] : w[4], upper, sel_bytes, sel);
             }
 #pragma unroll
-            for (int q = 4 * st; q < 4 * st + 4; ++q) a[q] = weight_pair(c[2 * q], c[2 * q + 1], th, tl);
+            for (int q = 4 * st; q < 4 * st + 4; ++q) a[q] = __builtin_amdgcn_perm(th, tl, sel[q]);
         }
     };
 
