@@ -481,7 +481,9 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
                   MatmulConfig, graph_of, time_graph, batch: int = 1) -> int:
     """Per configs[1] matrix: three cold launches of the M=1 GEMV (the LUT23
     kernel; with batch > 1 the kernel the library's dispatch picks, of which
-    the direct-fragment form is stamped) with the phase stamps of every wave
+    the direct-fragment and wide forms are stamped: the wide form's slot 3,
+    named for the GEMV's tables, is the other contributors' partials
+    published) with the phase stamps of every wave
     (100 MHz wall clock, lane 0) and the XCC it ran on. Wall clocks of different XCCs are not comparable,
     so every time is taken against the first wave start of the wave's own
     XCC: each phase's time, the XCC's span (first start to last stamp), each

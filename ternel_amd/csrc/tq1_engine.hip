@@ -1180,39 +1180,54 @@ constexpr int kDirectStride = kBlockWeights + 8;      // halves per staged activ
 // The 32 selector dwords of one half block (pairs of weights, in the direct K
 // order), from the selector tables in LDS (sel_bytes, tq1_bytes.h): u[0..3]
 // hold the half's twelve code bytes at bytes 2..13, w6 code byte 24 (byte 2)
-// and the tail byte (byte 3). Code bytes 2w, 2w+1 give pairs 5w .. 5w+4;
-// pairs 30 and 31 are code byte 24's first four weights in the lower half
-// and, in the upper half, its fifth with the three tail weights.
-__device__ __forceinline__ void half_block_selectors(const uint32_t (&u)[4], uint32_t w6, bool upper,
-                                                     const char *sel_bytes, uint32_t (&sel)[32]) {
-    auto lds = [&](uint32_t address, int entry) {
-        return *reinterpret_cast<const uint32_t *>(sel_bytes + address + entry * 4);
-    };
+// and the tail byte (byte 3). Code bytes 2w, 2w+1 (window w) give pairs
+// 5w .. 5w+4; pairs 30 and 31 are code byte 24's first four weights in the
+// lower half and, in the upper half, its fifth with the three tail weights.
+// The work comes in pieces that a caller can spread over its MFMA stages: the
+// split of windows 2k and 2k+1 (window_splits, VALU only), the five table
+// reads of one window (window_selectors) and the tail's (tail_selectors).
+// Selectors 5w+2 and 30 are the OR of two table reads; the pieces leave the
+// second in late[w] (late[6] for selector 30), for the consumer to OR in where
+// it takes the selector, rather than wait for the reads it has just issued.
+struct WindowSplits {
+    uint32_t la, ha, lb, hb;  // a / 9, a % 9, b / 27, b % 27 of both windows, one per 16-bit half
+};
+
+__device__ __forceinline__ WindowSplits window_splits(const uint32_t (&u)[4], int k) {
+    // the a bytes (even code bytes) of windows 2k, 2k+1 and their b bytes,
+    // one per 16-bit half
+    const u16x2 a = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(u[k + 1], u[k], 0x0c040c02u));
+    const u16x2 b = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(u[k + 1], u[k], 0x0c050c03u));
+    const u16x2 ha = tq1_bytes::lut23_high(a), la = tq1_bytes::lut23_low(a, ha);
+    const u16x2 hb = tq1_bytes::split27_high(b), lb = tq1_bytes::split27_low(b, hb);
+    return WindowSplits{__builtin_bit_cast(uint32_t, la), __builtin_bit_cast(uint32_t, ha),
+                        __builtin_bit_cast(uint32_t, lb), __builtin_bit_cast(uint32_t, hb)};
+}
+
+__device__ __forceinline__ uint32_t selector_lds(const char *sel_bytes, uint32_t address, int entry) {
+    return *reinterpret_cast<const uint32_t *>(sel_bytes + address + entry * 4);
+}
+
+// Window 2k + e of splits s (window_splits(u, k)): selectors 5w .. 5w+4.
+__device__ __forceinline__ void window_selectors(const WindowSplits &s, int k, int e, const char *sel_bytes,
+                                                 uint32_t (&sel)[32], uint32_t (&late)[7]) {
     const uint32_t zero = 0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        // the a bytes (even code bytes) of windows 2k, 2k+1 and their b bytes,
-        // one per 16-bit half
-        const u16x2 a = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(u[k + 1], u[k], 0x0c040c02u));
-        const u16x2 b = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(u[k + 1], u[k], 0x0c050c03u));
-        const u16x2 ha = tq1_bytes::lut23_high(a), la = tq1_bytes::lut23_low(a, ha);
-        const u16x2 hb = tq1_bytes::split27_high(b), lb = tq1_bytes::split27_low(b, hb);
-        const uint32_t la2 = __builtin_bit_cast(uint32_t, la), ha2 = __builtin_bit_cast(uint32_t, ha);
-        const uint32_t lb2 = __builtin_bit_cast(uint32_t, lb), hb2 = __builtin_bit_cast(uint32_t, hb);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int w = 2 * k + e;
-            const uint32_t al = e ? lut_address_hi(la2, zero) : lut_address_lo(la2, zero);
-            const uint32_t ah = e ? lut_address_hi(ha2, zero) : lut_address_lo(ha2, zero);
-            const uint32_t bl = e ? lut_address_hi(lb2, zero) : lut_address_lo(lb2, zero);
-            const uint32_t bh = e ? lut_address_hi(hb2, zero) : lut_address_lo(hb2, zero);
-            sel[5 * w] = lds(al, tq1_bytes::kSelT9a);
-            sel[5 * w + 1] = lds(ah, tq1_bytes::kSelT27aX);
-            sel[5 * w + 2] = lds(ah, tq1_bytes::kSelT27aY) | lds(bl, tq1_bytes::kSelT27bX);
-            sel[5 * w + 3] = lds(bl, tq1_bytes::kSelT27bY);
-            sel[5 * w + 4] = lds(bh, tq1_bytes::kSelT9b);
-        }
-    }
+    const int w = 2 * k + e;
+    const uint32_t al = e ? lut_address_hi(s.la, zero) : lut_address_lo(s.la, zero);
+    const uint32_t ah = e ? lut_address_hi(s.ha, zero) : lut_address_lo(s.ha, zero);
+    const uint32_t bl = e ? lut_address_hi(s.lb, zero) : lut_address_lo(s.lb, zero);
+    const uint32_t bh = e ? lut_address_hi(s.hb, zero) : lut_address_lo(s.hb, zero);
+    sel[5 * w] = selector_lds(sel_bytes, al, tq1_bytes::kSelT9a);
+    sel[5 * w + 1] = selector_lds(sel_bytes, ah, tq1_bytes::kSelT27aX);
+    sel[5 * w + 2] = selector_lds(sel_bytes, ah, tq1_bytes::kSelT27aY);
+    late[w] = selector_lds(sel_bytes, bl, tq1_bytes::kSelT27bX);
+    sel[5 * w + 3] = selector_lds(sel_bytes, bl, tq1_bytes::kSelT27bY);
+    sel[5 * w + 4] = selector_lds(sel_bytes, bh, tq1_bytes::kSelT9b);
+}
+
+// Selectors 30 and 31 from code byte 24 and the tail byte (w6).
+__device__ __forceinline__ void tail_selectors(uint32_t w6, bool upper, const char *sel_bytes, uint32_t (&sel)[32],
+                                               uint32_t (&late)[7]) {
     // (The half-dependent choices as bit blends with a lane mask: written as
     // selects, they became an exec-masked branch.)
     const uint32_t mask = 0u - static_cast<uint32_t>(upper);
@@ -1220,11 +1235,33 @@ __device__ __forceinline__ void half_block_selectors(const uint32_t (&u)[4], uin
     const uint32_t p24 = (w6 >> 16) & 0xffu;
     const uint32_t t = tq1_bytes::tail_entry(w6 >> 24);
     const uint32_t h24 = (p24 * 57u) >> 9, l24 = p24 - 9u * h24;
-    const uint32_t lead = lds(blend(4 * (t + tq1_bytes::kSelT27bX), 4 * (l24 + tq1_bytes::kSelT9a)), 0);
-    const uint32_t rest = lds(blend(4 * (t + tq1_bytes::kSelT27bY), 4 * (h24 + tq1_bytes::kSelT27aX)), 0);
-    const uint32_t fifth = lds(4 * h24, tq1_bytes::kSelT27aY);
-    sel[30] = lead | (fifth & mask);
+    const uint32_t lead =
+        selector_lds(sel_bytes, blend(4 * (t + tq1_bytes::kSelT27bX), 4 * (l24 + tq1_bytes::kSelT9a)), 0);
+    const uint32_t rest =
+        selector_lds(sel_bytes, blend(4 * (t + tq1_bytes::kSelT27bY), 4 * (h24 + tq1_bytes::kSelT27aX)), 0);
+    const uint32_t fifth = selector_lds(sel_bytes, 4 * h24, tq1_bytes::kSelT27aY);
+    sel[30] = lead;
+    late[6] = fifth & mask;
     sel[31] = rest;
+}
+
+// Selector q with its late part (see above).
+__device__ __forceinline__ uint32_t full_selector(const uint32_t (&sel)[32], const uint32_t (&late)[7], int q) {
+    return q == 30 ? sel[30] | late[6] : (q < 30 && q % 5 == 2 ? sel[q] | late[q / 5] : sel[q]);
+}
+
+__device__ __forceinline__ void half_block_selectors(const uint32_t (&u)[4], uint32_t w6, bool upper,
+                                                     const char *sel_bytes, uint32_t (&sel)[32]) {
+    uint32_t late[7];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const WindowSplits s = window_splits(u, k);
+        window_selectors(s, k, 0, sel_bytes, sel, late);
+        window_selectors(s, k, 1, sel_bytes, sel, late);
+    }
+    tail_selectors(w6, upper, sel_bytes, sel, late);
+#pragma unroll
+    for (int q = 0; q < 32; ++q) sel[q] = full_selector(sel, late, q);
 }
 
 // One pipeline step of direct_gemm_kernel: the MFMAs of the current group
@@ -1567,6 +1604,7 @@ constexpr size_t wide_lds_bytes(int nb) {
 constexpr int wide_frag_floats(int nb) { return nb * 16 * 64; }
 constexpr int kBufferRsrcFlags = 0x00020000;               // gfx9 raw buffer: 32-bit data format
 constexpr int kWideTileSlots = 8184;                       // stream-K counter pairs (arrivals, publications)
+constexpr int kXcds = 8;                                   // MI355X: 8 XCDs of 32 CUs, each with its own L2
 
 __device__ __forceinline__ int direct_target_unit(int u) { return u < 15 ? u : (u < 30 ? u + 1 : (u == 30 ? 15 : 31)); }
 
@@ -1661,11 +1699,23 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA bases go in M0
     const bool upper = lane >= 32;
     const int P = gridDim.x;
-    const int p = blockIdx.x;
+    // Workgroups go to the 8 XCDs round-robin by launch index; with this
+    // order each XCD runs one contiguous eighth of the unit sequence, so its
+    // L2 serves the activation blocks of its own tiles only and most tiles'
+    // contributors share an XCD. The results do not depend on the placement.
+    const int p = P % kXcds == 0 ? (blockIdx.x % kXcds) * (P / kXcds) + blockIdx.x / kXcds : blockIdx.x;
     const int G = geo.G;
     const int row_bytes = G * kBlockWeights * 2;  // one activation row
     const int u_begin = wide_unit_begin(geo.units, p, P);
     const int u_end = wide_unit_begin(geo.units, p + 1, P);
+    // Phase stamps of the profile build: 0 start, 1 the first unit's operands
+    // in LDS, 5 a segment summed, 7 its arrival counted; for a tile this
+    // workgroup reduces, 3 the others' partials published and 8 the tile
+    // stored (the last segment's stamps are the ones kept).
+    const int wide_wave_id = p * kWideWaves + wave;
+    (void)wide_wave_id;
+    TQ1_PHASE(wide_wave_id, 0);
+    TQ1_PHASE_XCC(wide_wave_id);
     if (u_begin >= u_end) return;
     const int last_u = u_end - 1;
 
@@ -1758,11 +1808,16 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
 
     // One group step on a single register buffer `a` (32 dwords): stage st
     // runs MFMA step st of the current group from dwords 4st..4st+3
-    // (activation buffer buf) and then decodes the same dwords of the next
-    // group's words w over them.
+    // (activation buffer buf). The decode of the next group's words w
+    // overwrites dwords 4(st-1)..4(st-1)+3 at stage st (the last stage its
+    // own as well), a stage after the MFMAs that read them, and the selector
+    // table reads of each window run a stage or more ahead of the perms that
+    // take them: no stage waits on the LDS between its MFMAs.
     auto step = [&](uint32_t (&a)[32], const uint32_t (&w)[5], int buf, bool mfma) {
         uint32_t th = 0, tl = 0;
-        uint32_t sel[32];
+        uint32_t sel[32], late[7];
+        const uint32_t u[4] = {w[0], w[1], w[2], w[3]};
+        WindowSplits sp;
         const _Float16 *xb = reinterpret_cast<const _Float16 *>(xbuf0 + buf * kXBytes);
         auto frag = [&](int st, int nb) {
             return *reinterpret_cast<const half8 *>(xb + nb * 32 * kBlockWeights + frag_row + ((st ^ frag_l7) * 8));
@@ -1837,13 +1892,31 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                     if (st < 7) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
                 }
             }
+            // selectors of windows 0-1 at stage 0, 2 at 1, 3 at 2, 4 at 3, 5 at
+            // 4 and the tail's at 5; stage st's perms take selectors
+            // 4(st-1) .. 4(st-1)+3, which come from windows read by stage st-1
             if (st == 0) {
                 scale_tables((upper ? w[4] : w[0]) & 0xffffu, th, tl);
-                const uint32_t u[4] = {w[0], w[1], w[2], w[3]};
-                half_block_selectors(u, upper ? w[3] : w[4], upper, sel_bytes, sel);
+                sp = window_splits(u, 0);
+                window_selectors(sp, 0, 0, sel_bytes, sel, late);
+                window_selectors(sp, 0, 1, sel_bytes, sel, late);
+            } else if (st == 1 || st == 3) {
+                sp = window_splits(u, (st + 1) / 2);
+                window_selectors(sp, (st + 1) / 2, 0, sel_bytes, sel, late);
+            } else if (st == 2 || st == 4) {
+                window_selectors(sp, st / 2, 1, sel_bytes, sel, late);
+            } else if (st == 5) {
+                tail_selectors(upper ? w[3] : w[4], upper, sel_bytes, sel, late);
             }
+            if (st > 0) {
 #pragma unroll
-            for (int q = 4 * st; q < 4 * st + 4; ++q) a[q] = __builtin_amdgcn_perm(th, tl, sel[q]);
+                for (int q = 4 * (st - 1); q < 4 * st; ++q)
+                    a[q] = __builtin_amdgcn_perm(th, tl, full_selector(sel, late, q));
+            }
+            if (st == 7) {
+#pragma unroll
+                for (int q = 28; q < 32; ++q) a[q] = __builtin_amdgcn_perm(th, tl, full_selector(sel, late, q));
+            }
         }
     };
 
@@ -1929,6 +2002,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             s_last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                      static_cast<unsigned>(q1 - q0);
         __syncthreads();
+        TQ1_PHASE(wide_wave_id, 7);
         if (!s_last) {
             const int base = slot_base(p, seg_begin == u_begin ? 0 : 1);
 #pragma unroll
@@ -1961,6 +2035,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                 __hip_atomic_fetch_or(counters + kWorkspaceErrorSlot, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
+        TQ1_PHASE(wide_wave_id, 3);
         const bool published = s_published;
         // The sum runs in workgroup order q0..q1: the partials of q0..p-1, this
         // workgroup's accumulators, then the partials of p+1..q1. It is formed
@@ -2023,6 +2098,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(counters + kWideTileSlots + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        TQ1_PHASE(wide_wave_id, 8);
     };
 
     // Prefetch cursors: activations kRing - 1 units ahead, words kRing; no
@@ -2050,6 +2126,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         }
         wait_vector_memory();
         __syncthreads();
+        TQ1_PHASE(wide_wave_id, 1);
         uint32_t w[5];
         read_words(w, u_begin & (kRing - 1));
         step(a, w, u_begin & (kRing - 1), false);  // decode only (0 * inf activations would be NaN)
@@ -2095,6 +2172,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             asm volatile("s_barrier" ::: "memory");
             publish();
         }
+        TQ1_PHASE(wide_wave_id, 5);
         emit(t, seg_begin, seg_end);
     }
     wait_vector_memory();
