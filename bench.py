@@ -65,7 +65,7 @@ def parse() -> argparse.Namespace:
                         "graph-timed stream GEMV and LUT23 kernel")
     p.add_argument("--phase-batch", type=int, default=1,
                    help="activation rows of the --phase-profile launches: 1 profiles the LUT23 GEMV, more the "
-                        "kernel the library's dispatch picks for that batch (stamped: the direct-fragment form)")
+                        "kernel the library's dispatch picks for that batch (stamped: the direct-fragment and wide forms)")
     p.add_argument("--prefill-probe", action="store_true",
                    help="run only the M=512 prefill GEMMs (gate/up, down), 2 warm-up + --steps eager launches "
                         "each, for rocprofv3 --pmc MFMA-utilisation passes")
@@ -475,15 +475,17 @@ def main() -> int:
 
 PHASES = ("start", "activations arrived", "first words issued", "own tables written", "tables ready (barrier)",
           "blocks summed", "partial stored and acknowledged", "arrival counted", "fix-up done")
+# The wide form's stamps in the same slots (2-4 unused; 7 and 8 only where it reduces a shared tile).
+WIDE_PHASES = ("start", "first unit's operands in LDS", "-", "-", "-", "segment summed", "arrival counted",
+               "other contributors' partials published", "tile stored")
 
 
 def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_linear_words, PackedTensorLayout,
                   MatmulConfig, graph_of, time_graph, batch: int = 1) -> int:
     """Per configs[1] matrix: three cold launches of the M=1 GEMV (the LUT23
     kernel; with batch > 1 the kernel the library's dispatch picks, of which
-    the direct-fragment and wide forms are stamped: the wide form's slot 3,
-    named for the GEMV's tables, is the other contributors' partials
-    published) with the phase stamps of every wave
+    the direct-fragment and wide forms are stamped, the wide form with its own
+    phase names) with the phase stamps of every wave
     (100 MHz wall clock, lane 0) and the XCC it ran on. Wall clocks of different XCCs are not comparable,
     so every time is taken against the first wave start of the wave's own
     XCC: each phase's time, the XCC's span (first start to last stamp), each
@@ -510,6 +512,8 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
                 "p95_us": round(values[int(0.95 * (len(values) - 1))], 2), "max_us": round(values[-1], 2)}
 
     for i, (name, K, N) in enumerate(C1_SHAPES):
+        wide = batch > 1 and handle.ternel_tq1_linear_kernel(batch, N, K, 0) == 3  # TERNEL_TQ1_GEMM_WIDE
+        names = WIDE_PHASES if wide else PHASES
         lay = PackedTensorLayout.for_tensor(N, K)
         weights = [pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
                    for r in range(ring)]
@@ -519,7 +523,7 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
             return tq1_matmul_words(w, x, layout=lay) if batch == 1 else tq1_linear_words(w, x, layout=lay)
 
         graph_ms = time_graph(graph_of(lambda: [gemv(weights[r % ring]) for r in range(ring * 4)])) / (ring * 4)
-        phase_times = {phase: [] for phase in PHASES}
+        phase_times = {phase: [] for phase in names if phase != "-"}
         spans, durations, by_start = [], {}, [[] for _ in range(4)]
         for r in range(3):  # three cold launches, each over a copy last read 13 launches ago
             fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
@@ -530,9 +534,10 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
             for xcc in {st[slots - 1] for st in stamps}:
                 mine = [st for st in stamps if st[slots - 1] == xcc]
                 t0 = min(st[0] for st in mine)
-                spans.append(max(max(v for v in st[:len(PHASES)] if v) for st in mine) / 100 - t0 / 100)
-                for p, phase in enumerate(PHASES):
-                    phase_times[phase] += [(st[p] - t0) / 100 for st in mine if st[p]]
+                spans.append(max(max(v for v in st[:len(names)] if v) for st in mine) / 100 - t0 / 100)
+                for p, phase in enumerate(names):
+                    if phase != "-":
+                        phase_times[phase] += [(st[p] - t0) / 100 for st in mine if st[p]]
                 ranked = sorted(mine, key=lambda st: st[0])
                 quarter = max(1, len(ranked) // 4)
                 for q in range(4):
@@ -540,9 +545,9 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
                     by_start[q] += [((st[0] - t0) / 100, (st[3] - st[0]) / 100, (st[1] - st[0]) / 100,
                                      (st[2] - st[1]) / 100) for st in part if st[3] and st[1] and st[2]]
             for st in stamps:  # between consecutive phases the wave stamped
-                present = [p for p in range(len(PHASES)) if st[p]]
+                present = [p for p in range(len(names)) if st[p]]
                 for a, b in zip(present, present[1:]):
-                    durations.setdefault(f"{PHASES[a]} -> {PHASES[b]}", []).append((st[b] - st[a]) / 100)
+                    durations.setdefault(f"{names[a]} -> {names[b]}", []).append((st[b] - st[a]) / 100)
         print(json.dumps({
             "phase_profile": name, "K": K, "N": N, "M": batch, "waves_per_launch": len(phase_times["start"]) // 3,
             "gemv_graph_us": round(graph_ms * 1e3, 3),

@@ -1256,12 +1256,14 @@ __device__ __forceinline__ void half_block_selectors(const uint32_t (&u)[4], uin
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const WindowSplits s = window_splits(u, k);
-        window_selectors(s, k, 0, sel_bytes, sel, late);
-        window_selectors(s, k, 1, sel_bytes, sel, late);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            window_selectors(s, k, e, sel_bytes, sel, late);
+            sel[5 * (2 * k + e) + 2] |= late[2 * k + e];
+        }
     }
     tail_selectors(w6, upper, sel_bytes, sel, late);
-#pragma unroll
-    for (int q = 0; q < 32; ++q) sel[q] = full_selector(sel, late, q);
+    sel[30] |= late[6];
 }
 
 // One pipeline step of direct_gemm_kernel: the MFMAs of the current group
@@ -1709,8 +1711,8 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     const int u_begin = wide_unit_begin(geo.units, p, P);
     const int u_end = wide_unit_begin(geo.units, p + 1, P);
     // Phase stamps of the profile build: 0 start, 1 the first unit's operands
-    // in LDS, 5 a segment summed, 7 its arrival counted; for a tile this
-    // workgroup reduces, 3 the others' partials published and 8 the tile
+    // in LDS, 5 a segment summed, 6 its arrival counted; for a tile this
+    // workgroup reduces, 7 the others' partials published and 8 the tile
     // stored (the last segment's stamps are the ones kept).
     const int wide_wave_id = p * kWideWaves + wave;
     (void)wide_wave_id;
@@ -2002,7 +2004,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             s_last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                      static_cast<unsigned>(q1 - q0);
         __syncthreads();
-        TQ1_PHASE(wide_wave_id, 7);
+        TQ1_PHASE(wide_wave_id, 6);
         if (!s_last) {
             const int base = slot_base(p, seg_begin == u_begin ? 0 : 1);
 #pragma unroll
@@ -2035,7 +2037,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                 __hip_atomic_fetch_or(counters + kWorkspaceErrorSlot, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
-        TQ1_PHASE(wide_wave_id, 3);
+        TQ1_PHASE(wide_wave_id, 7);
         const bool published = s_published;
         // The sum runs in workgroup order q0..q1: the partials of q0..p-1, this
         // workgroup's accumulators, then the partials of p+1..q1. It is formed
