@@ -955,6 +955,8 @@ __global__ __launch_bounds__(kThreads) void reduce_partials_kernel(const float *
 // ---------------------------------------------------------------------------
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((vector_size(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
@@ -1170,6 +1172,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 // bytes, the other selects from {-s, z, +s} as in the LDS-tile form. Illegal
 // bytes give arbitrary digits in 0..2, so nothing is ever indexed by them.
 // ---------------------------------------------------------------------------
+constexpr int kBufferRsrcFlags = 0x00020000;  // gfx9 raw buffer resource: 32-bit data format
 constexpr int kDirectWaves = 4;
 constexpr int kDirectThreads = kDirectWaves * 64;
 constexpr int kDirectRows = kDirectWaves * 32;          // weight rows per workgroup
@@ -1486,22 +1489,35 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
     // D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) % 2), item 4 * (i / 8) + i % 4;
     // here i is a weight row of the wave and j an activation row.
     if (k_split > 1) {
-        // Partials in fragment order, only the lanes of real activation rows:
-        // item r of tile nb in lane j + 32 h goes to ((nb * 16 + r) * 2 + h) * S
-        // + j with S = min(M, 32), so a batch of 8 writes a quarter of the 32
-        // columns an MFMA tile holds (each lane re-reads its own).
+        // Partials in quads, only the lanes of real activation rows: values
+        // 4q .. 4q+3 of tile nb in lane j + 32 h (j < S = min(M, 32)) sit at
+        // ((nb * 4 + q) * 2 S + h * S + j) * 4 of the (chunk, wave) region, so
+        // a lane stores and loads them with four 16-byte device-coherent (sc1)
+        // buffer accesses, each instruction covering 2 S * 16 contiguous bytes.
+        // The chunk, tile and quad offsets are wave-uniform (scalar).
+        constexpr int kDeviceCoherent = 16;  // cache policy SC1
         const int S = min(M, 32);
         const int frag = NB * 32 * S;
+        const int64_t chunk_stride = static_cast<int64_t>(kDirectWaves) * frag;
         const int j = lane & 31;
-        const int slot = (lane >> 5) * S + j;
-        float *mine = partial + ((static_cast<int64_t>(blockIdx.x) * k_split + blockIdx.y) * kDirectWaves + wave) * frag + slot;
+        const float *wave_base = partial + static_cast<int64_t>(blockIdx.x) * k_split * chunk_stride +
+                                 static_cast<int64_t>(wave) * frag;
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(wave_base), 0, static_cast<int>(k_split * chunk_stride * 4), kBufferRsrcFlags);
+        // lanes past the real rows load row S - 1 again (never stored)
+        const uint32_t voff = static_cast<uint32_t>(((lane >> 5) * S + min(j, S - 1)) * 16);
+        auto value_offset = [&](int z, int nb, int q) {
+            return static_cast<int>((z * chunk_stride + (nb * 4 + q) * 2 * S * 4) * 4);
+        };
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
             if (nb * 32 + j < M)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    __hip_atomic_store(mine + (nb * 16 + r) * 2 * S, acc[nb][r], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 v4 = {acc[nb][4 * q], acc[nb][4 * q + 1], acc[nb][4 * q + 2], acc[nb][4 * q + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v4), rp, voff,
+                                                           value_offset(blockIdx.y, nb, q), kDeviceCoherent);
+                }
         wait_vector_memory();
         TQ1_PHASE(direct_wave_id, 6);  // partial stored and acknowledged
         __syncthreads();
@@ -1512,34 +1528,59 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
         __syncthreads();
         TQ1_PHASE(direct_wave_id, 7);  // arrival counted
         if (!s_last) return;
-        const float *base = partial + (static_cast<int64_t>(blockIdx.x) * k_split * kDirectWaves + wave) * frag + slot;
-        const int64_t chunk_stride = static_cast<int64_t>(kDirectWaves) * frag;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
-        // The chunks are added in chunk order, kBatch of them per memory
-        // round trip (all their loads issued before the first add; a batch
-        // past the last chunk re-reads it and adds nothing).
-        constexpr int kBatch = NB == 1 ? 8 : 4;
-        for (int z0 = 0; z0 < k_split; z0 += kBatch) {
-            float v[kBatch][NB][16];
+        // The chunks are added in chunk order, all loads of a batch issued
+        // before its first add (a batch past the last chunk re-reads it and
+        // adds nothing): one tile and up to 8 chunks in one batch; more chunks
+        // (down: 17) one half of the 16 values at a time with up to 17 chunks
+        // of it per batch, 34 loads in flight; two tiles 4 chunks per batch.
+        auto load4 = [&](int z, int nb, int q) {
+            return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rp, voff, value_offset(min(z, k_split - 1), nb, q),
+                                                 kDeviceCoherent));
+        };
+        if (NB == 1 && k_split > 8) {
+            constexpr int kHalfBatch = 17;
+            for (int z0 = 0; z0 < k_split; z0 += kHalfBatch) {
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
+                for (int h = 0; h < 2; ++h) {
+                    f32x4 v[kHalfBatch][2];
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
+                    for (int u = 0; u < kHalfBatch; ++u)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        v[u][nb][r] = __hip_atomic_load(base + min(z0 + u, k_split - 1) * chunk_stride +
-                                                            (nb * 16 + r) * 2 * S,
-                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        for (int q = 0; q < 2; ++q) v[u][q] = load4(z0 + u, 0, 2 * h + q);
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                if (z0 + u < k_split)
+                    for (int u = 0; u < kHalfBatch; ++u)
+                        if (z0 + u < k_split)
+#pragma unroll
+                            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[0][8 * h + 4 * q + e] += v[u][q][e];
+                }
+            }
+        } else {
+            constexpr int kBatch = NB == 1 ? 8 : 4;
+            for (int z0 = 0; z0 < k_split; z0 += kBatch) {
+                f32x4 v[kBatch][NB][4];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u)
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[nb][r] += v[u][nb][r];
+                        for (int q = 0; q < 4; ++q) v[u][nb][q] = load4(z0 + u, nb, q);
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u)
+                    if (z0 + u < k_split)
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[nb][4 * q + e] += v[u][nb][q][e];
+            }
         }
         if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         TQ1_PHASE(direct_wave_id, 8);  // fix-up sums done
@@ -1604,7 +1645,6 @@ constexpr size_t wide_lds_bytes(int nb) {
     return wide_ring(nb) * (static_cast<size_t>(wide_x_bytes(nb)) + kWideWBytes);
 }
 constexpr int wide_frag_floats(int nb) { return nb * 16 * 64; }
-constexpr int kBufferRsrcFlags = 0x00020000;               // gfx9 raw buffer: 32-bit data format
 constexpr int kWideTileSlots = 8184;                       // stream-K counter pairs (arrivals, publications)
 constexpr int kXcds = 8;                                   // MI355X: 8 XCDs of 32 CUs, each with its own L2
 
@@ -1664,8 +1704,6 @@ __device__ __forceinline__ void pin_decoded(const uint32_t (&a)[32]) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
-typedef uint32_t u32x4 __attribute__((vector_size(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte-per-lane LDS-DMA through a buffer resource (gfx950). A plain
 // function, so that its arguments are checked once and not per template
