@@ -548,6 +548,13 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
                 present = [p for p in range(len(names)) if st[p]]
                 for a, b in zip(present, present[1:]):
                     durations.setdefault(f"{names[a]} -> {names[b]}", []).append((st[b] - st[a]) / 100)
+        if not spans:  # the dispatch picked a kernel without phase stamps (the tile form)
+            print(json.dumps({"phase_profile": name, "K": K, "N": N, "M": batch,
+                              "kernel": handle.ternel_tq1_linear_kernel(batch, N, K, 0),
+                              "note": "no phase stamps: the kernel the dispatch picks here is not stamped"}),
+                  flush=True)
+            del weights
+            continue
         print(json.dumps({
             "phase_profile": name, "K": K, "N": N, "M": batch, "waves_per_launch": len(phase_times["start"]) // 3,
             "gemv_graph_us": round(graph_ms * 1e3, 3),

@@ -1518,7 +1518,11 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v4), rp, voff,
                                                            value_offset(blockIdx.y, nb, q), kDeviceCoherent);
                 }
+        // Every store acknowledged at the coherence point before the arrival
+        // is counted; the compiler barriers keep the stores above the wait.
+        asm volatile("" ::: "memory");
         wait_vector_memory();
+        asm volatile("" ::: "memory");
         TQ1_PHASE(direct_wave_id, 6);  // partial stored and acknowledged
         __syncthreads();
         unsigned *counter = counters + blockIdx.x;
