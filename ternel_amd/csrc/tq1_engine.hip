@@ -962,11 +962,13 @@ constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
 constexpr int kGemmStride = kBlockWeights + 8;  // halves per LDS row
 
-// Digit carriers (see the direct-fragment form below for the method): for a
-// byte p <= 242, t = p * 69043 approximates p / 243 in 24-bit fixed point and
-// each t = (t mod 2^24) * 3 leaves the next base-3 digit, most significant
-// first, in bits 24-25 (exact for every legal byte; the tail byte p <= 26 uses
-// 9 * 69043). Two carriers become two fp16 weights with two v_perm_b32.
+// Digit carriers: for a byte p <= 242, t = p * 69043 approximates p / 243 in
+// 24-bit fixed point and each t = (t mod 2^24) * 3 -- one v_mul_u32_u24,
+// which ignores the bits above 24 -- leaves the next base-3 digit, most
+// significant first, in bits 24-25 (exact for every legal byte, checked
+// exhaustively on the CPU; the tail byte p <= 26 uses 9 * 69043; illegal
+// bytes give digits in 0..2). Two carriers become two fp16 weights with two
+// v_perm_b32: one gathers their top bytes, the other selects from the table.
 using tq1_bytes::byte_digit_carriers;
 using tq1_bytes::tail_digit_carriers;
 
@@ -1148,10 +1150,11 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 // Weights never touch LDS: each lane decodes half of one block straight into
 // the A operand of v_mfma_f32_32x32x16_f16 (weight rows x K); the activations
 // are the B operand (K x batch). A workgroup (4 waves, 128 weight rows) copies
-// its K chunk of activations into LDS once, with LDS-DMA loads (one padded
-// row per instruction, no registers), then each wave runs its groups with no
-// barrier: a wave owns 32 weight rows, lane l decodes half h = l / 32 of row
-// l % 32's block and reads 5 of the block's 7 words. NB = ceil(M / 32) tiles.
+// a window of its K chunk's activations into LDS (through registers for up to
+// 16 rows, by LDS-DMA for more), then each wave runs the window's groups with
+// no barrier: a wave owns 32 weight rows, lane l decodes half h = l / 32 of
+// row l % 32's block and reads 5 of the block's 7 words. NB = ceil(M / 32)
+// tiles.
 //
 // K order. The dot product over a group does not depend on the order of its
 // 128 terms, so both operands use one fixed permutation that makes the two
@@ -1163,14 +1166,14 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 // in that order: logical 4-half unit u holds physical unit u (u < 15), 30
 // (u = 15), u - 1 (16 <= u < 31) or 31 (u = 31).
 //
-// Digits. For a byte p <= 242, t = p * 69043 approximates p / 243 in 24-bit
-// fixed point (exact digits for every legal byte, checked exhaustively), and
-// each step t = (t mod 2^24) * 3 -- one v_mul_u32_u24, which ignores the bits
-// above 24 -- leaves the next base-3 digit, most significant first, in bits
-// 24-25. The tail byte (p <= 26) uses 621387 = 9 * 69043. Two such digit
-// carriers become two fp16 weights with two v_perm_b32: one gathers their top
-// bytes, the other selects from {-s, z, +s} as in the LDS-tile form. Illegal
-// bytes give arbitrary digits in 0..2, so nothing is ever indexed by them.
+// Weights. A lane turns its half block into 32 dwords of fp16 weight pairs:
+// each pair of code bytes is split two bytes per 16-bit-packed operation and
+// indexes six small selector tables in LDS (tq1_bytes.h, half_block_selectors
+// below), and one v_perm_b32 per pair selects the pair's two fp16 values from
+// {-s, z, +s} (z is 0, or NaN for a non-finite scale, as (t - 1) * s gives).
+// Every byte value, legal or not, indexes inside the tables (checked on the
+// CPU over all of them). The wide form decodes the same way; the LDS-tile
+// form keeps the 24-bit digit carriers of tq1_bytes.h.
 // ---------------------------------------------------------------------------
 constexpr int kBufferRsrcFlags = 0x00020000;  // gfx9 raw buffer resource: 32-bit data format
 constexpr int kDirectWaves = 4;
@@ -1652,7 +1655,6 @@ constexpr int wide_frag_floats(int nb) { return nb * 16 * 64; }
 constexpr int kWideTileSlots = 8184;                       // stream-K counter pairs (arrivals, publications)
 constexpr int kXcds = 8;                                   // MI355X: 8 XCDs of 32 CUs, each with its own L2
 
-__device__ __forceinline__ int direct_target_unit(int u) { return u < 15 ? u : (u < 30 ? u + 1 : (u == 30 ? 15 : 31)); }
 
 struct WideGeometry {
     int M, N, G;
@@ -1881,7 +1883,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
             // Stages are scheduling regions: the decode of a stage is not
-            // hoisted into earlier ones (its carriers would all be live at
+            // hoisted into earlier ones (its selectors would all be live at
             // once).
             __builtin_amdgcn_sched_barrier(0);
             if (NB < 8 && mfma) {
