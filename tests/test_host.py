@@ -247,6 +247,12 @@ def test_workspace_queries() -> None:
     # partials of the 8 real activation columns only
     assert handle.ternel_tq1_gemm_workspace_bytes(8, 256, 5120, direct, 5) == counters + 5 * 2 * 128 * 8 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(40, 300, 5120, direct, 4) == counters + 4 * 3 * 128 * 64 * 4
+    # auto split: the smallest with chunks of a multiple of 8 groups (of 4 at 17-32 rows) that
+    # reaches 512 workgroups -- gate/up 136 row blocks x 5 at any batch, QKV at 32 rows 64 x 10
+    assert handle.ternel_tq1_gemm_workspace_bytes(16, 17408, 5120, direct, 0) == counters + 5 * 136 * 128 * 16 * 4
+    assert handle.ternel_tq1_gemm_workspace_bytes(32, 17408, 5120, direct, 0) == counters + 5 * 136 * 128 * 32 * 4
+    assert handle.ternel_tq1_gemm_workspace_bytes(16, 8192, 5120, direct, 0) == counters + 5 * 64 * 128 * 16 * 4
+    assert handle.ternel_tq1_gemm_workspace_bytes(32, 8192, 5120, direct, 0) == counters + 10 * 64 * 128 * 32 * 4
     assert handle.ternel_tq1_gemm_workspace_bytes(65, 256, 5120, direct, 1) == 0  # rejected
     # wide form: two fp32 partial slots of 8 waves x NB fragments x 16 x 64 per
     # workgroup (one per CU, 256 without a GPU, at most one per unit), then
