@@ -2620,6 +2620,10 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
     plan->chunk_groups = static_cast<int>(G / k_split);
     const size_t group_bytes = static_cast<size_t>(plan->staged_rows) * kDirectStride * sizeof(_Float16);
     int window = static_cast<int>(kDirectLdsBytes / group_bytes);
+    // Two tiles (64 staged rows): windows of 4 groups, so that two workgroups
+    // fit a CU's LDS (69.6 KiB each, against one at 8 groups); measured on
+    // MI355X, gate/up M=40 38.4 us against 53.0, QKV 24.9 against 35.7.
+    if (plan->nb == 2 && window > 4) window = 4;
     if (window >= plan->chunk_groups)
         window = plan->chunk_groups;
     else if (window >= 8)
@@ -2767,7 +2771,11 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
 
 // Automatic choice, from a sweep of every form over the 27B linears on MI355X
 // (the fixture tests/golden/dispatch_sweep_mi355x.json replays it): the direct
-// form up to 32 activation rows; above, the wide form when stream-K has enough
+// form up to 32 activation rows, and up to 64 for matrices under 16 MiB of
+// packed weights (O 8192->5120 M=40-64: 26.5-28.2 us against the wide form's
+// 29.4-30.8 and the tile form's 29.4-32.7; QKV within 0.5 % of the fastest,
+// while gate/up and down stay faster on the wide form); above, the wide form
+// when stream-K has enough
 // tiles or enough work per CU to amortise its reduction -- at least CUs/4
 // tiles (a tile's partials come from at most ~4 contributors) or 15 (tile,
 // group) steps per CU -- and the fixed-split tile form otherwise (QKV
@@ -2775,11 +2783,15 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
 // against 57.7 the other way). The tile form also serves a fixed K split and
 // rows too long for the wide form's 32-bit buffer offsets.
 constexpr int64_t kAutoDirectMaxBatch = 32;
+constexpr int64_t kAutoDirectMaxBatchSmall = 64;
+constexpr int64_t kAutoSmallMatrixBytes = 16ll << 20;
 int wide_blocks(int64_t M, int64_t tiles_n, int64_t groups, int64_t cus);
 int device_cu_count();
 int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (form != TERNEL_TQ1_GEMM_AUTO) return form;
     if (M <= kAutoDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
+    const int64_t bytes = rows * (columns / kBlockWeights) * kBlockBytes;
+    if (M <= kAutoDirectMaxBatchSmall && bytes < kAutoSmallMatrixBytes) return TERNEL_TQ1_GEMM_DIRECT;
     if (k_split > 1 || columns > kWideMaxColumns) return TERNEL_TQ1_GEMM_TILE;
     const int64_t cus = device_cu_count();
     const int64_t groups = columns / kBlockWeights;
