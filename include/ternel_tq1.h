@@ -192,7 +192,8 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
  *                          with an ordered in-launch reduction (k_split must
  *                          be 0/1; columns < 2^22);
  *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 32 (M <= 64 for matrices under
- *                          16 MiB of packed weights); above, WIDE when it has at
+ *                          16 MiB of packed weights), but WIDE at 17-32 rows
+ *                          when rows / 256 reaches CUs/4; above, WIDE when it has at
  *                          least CUs/4 output tiles or 10 (tile, group) steps
  *                          per CU (15 at 128- or 256-wide tiles), TILE
  *                          otherwise (and when k_split > 1).
