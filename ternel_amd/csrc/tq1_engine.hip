@@ -1731,6 +1731,11 @@ __device__ __forceinline__ void buffer_dma16(__amdgpu_buffer_rsrc_t rsrc, void *
                                              uint32_t soffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)lds, 16, voffset, soffset, 0, 0);
 }
+// The same with 4 bytes per lane (one 256-byte row of a group per instruction).
+__device__ __forceinline__ void buffer_dma4(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voffset,
+                                            uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)lds, 4, voffset, soffset, 0, 0);
+}
 
 template <int NB>
 __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
@@ -1799,26 +1804,51 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
 
     unsigned char *const xbuf0 = wide_lds;
     unsigned char *const wbuf0 = wide_lds + kRing * kXBytes;
-    // DMA of a group's activation tile: 8 NB blocks of 1 KiB (4 rows), NB per
-    // wave; lane l of block b fills row 4b + l/16, stored chunk l%16. Block
-    // b = NB w + j starts at row 4b: the lane part of the offset depends on
-    // b % 4 only (row % 16), the rest (16 (b / 4) rows) is uniform.
-    constexpr int kVoff = NB % 4 == 0 ? 4 : NB;
+    // DMA of a group's activation tile, row r of it at byte 256 r with its
+    // 16-byte chunks XOR-swizzled by r mod 16 (logical chunk c at c ^ (r % 16)).
+    // Four or eight blocks read the permuted copy xp (the direct K order) by
+    // 16-byte DMA: 8 NB blocks of 1 KiB (4 rows), NB per wave; lane l of
+    // block b fills row 4b + l/16, stored chunk l%16. Block b = NB w + j starts
+    // at row 4b: the lane part of the offset depends on b % 4 only (row % 16),
+    // the rest (16 (b / 4) rows) is uniform. One or two blocks read x itself by
+    // 4-byte DMA, one row per instruction, each lane fetching the dword its
+    // swizzled position holds in the K order -- no pre-pass, whose launch
+    // would cost more than these few rows.
+    constexpr bool kDirectX = NB <= 2;
+    constexpr int kRowsPerWave = kCols / kWideWaves;  // 4 or 8 when kDirectX
+    constexpr int kVoff = kDirectX ? kRowsPerWave : (NB % 4 == 0 ? 4 : NB);
+    constexpr int kXDmaPerWave = kDirectX ? kRowsPerWave : NB;
     uint32_t voff_x[kVoff];
 #pragma unroll
     for (int j = 0; j < kVoff; ++j) {
-        const int row = 4 * ((wave * NB + j) & 3) + (lane >> 4);
-        voff_x[j] = static_cast<uint32_t>(row * row_bytes + (((lane & 15) ^ (row & 15)) * 16));
+        if (kDirectX) {
+            const int row = wave * kRowsPerWave + j;
+            const int chunk = (lane >> 2) ^ (row & 15);  // logical chunk at position lane / 4
+            const int unit = direct_source_unit(2 * chunk + ((lane >> 1) & 1));
+            voff_x[j] = static_cast<uint32_t>(unit * 8 + (lane & 1) * 4);
+        } else {
+            const int row = 4 * ((wave * NB + j) & 3) + (lane >> 4);
+            voff_x[j] = static_cast<uint32_t>(row * row_bytes + (((lane & 15) ^ (row & 15)) * 16));
+        }
     }
     auto issue_x = [&](const Cursor &c, int buf) {
         const int m0 = c.tm * kCols;
         const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<_Float16 *>(xp) + static_cast<int64_t>(m0) * (row_bytes / 2), 0,
             min(kCols, geo.M - m0) * row_bytes, kBufferRsrcFlags);
+        if constexpr (kDirectX) {
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int b = wave * NB + j;
-            buffer_dma16(rx, xbuf0 + buf * kXBytes + b * 1024, voff_x[j % kVoff], (b >> 2) * 16 * row_bytes + c.g * 256);
+            for (int j = 0; j < kRowsPerWave; ++j) {
+                const int r = wave * kRowsPerWave + j;
+                buffer_dma4(rx, xbuf0 + buf * kXBytes + r * 256, voff_x[j], r * row_bytes + c.g * 256);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int b = wave * NB + j;
+                buffer_dma16(rx, xbuf0 + buf * kXBytes + b * 1024, voff_x[j % kVoff],
+                             (b >> 2) * 16 * row_bytes + c.g * 256);
+            }
         }
     };
     // DMA of a group's words: 64-row block b = wave / 2, words 0-3 by the even
@@ -2196,7 +2226,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     // words of u+2 -- issued kRing - 2 steps earlier, or before the loop --
     // must have landed; the DMAs of the kRing - 2 later steps may stay in
     // flight (gfx9 encoding: vmcnt bits 3:0 and 15:14, other counters idle).
-    constexpr int kInFlight = (kRing - 2) * (NB + 4);
+    constexpr int kInFlight = (kRing - 2) * (kXDmaPerWave + 4);
     constexpr unsigned kWaitRing = (kInFlight & 15) | ((kInFlight >> 4) << 14) | 0x0f70;
     static_assert(kInFlight <= 63, "vmcnt holds at most 63");
     // Segments: maximal runs of this workgroup's units within one tile; the
@@ -2729,8 +2759,9 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
     plan->workgroups = static_cast<int>(wgs);
     // two partial slots per workgroup, each all of its waves' accumulators
     plan->partial_bytes = static_cast<size_t>(wgs) * 2 * kWideWaves * wide_frag_floats(plan->nb) * sizeof(float);
-    // the permuted copy of the activations follows the partials
-    plan->xp_bytes = static_cast<size_t>(M) * columns * sizeof(_Float16);
+    // the permuted copy of the activations follows the partials (four or
+    // eight blocks; one or two read x itself)
+    plan->xp_bytes = plan->nb <= 2 ? 0 : static_cast<size_t>(M) * columns * sizeof(_Float16);
     return TERNEL_TQ1_OK;
 }
 
@@ -2749,12 +2780,16 @@ int launch_wide_kernel(const uint32_t *packed, const _Float16 *xp, void *y, floa
 int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &plan, void *ws, hipStream_t stream) {
     unsigned *counters = static_cast<unsigned *>(ws);
     float *partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kPartialOffset);
-    _Float16 *xp = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kPartialOffset + plan.partial_bytes);
-    const int64_t quads = static_cast<int64_t>(plan.geo.M) * plan.geo.G * 8;  // 32-byte runs of the copy
-    hipLaunchKernelGGL(permute_activations_kernel, dim3(static_cast<unsigned>(ceil_div(quads, kThreads))),
-                       dim3(kThreads), 0, stream, static_cast<const uint2 *>(x), reinterpret_cast<uint2 *>(xp), quads,
-                       static_cast<int>(reinterpret_cast<uintptr_t>(xp) % 16 == 0));
-    TQ1_LAUNCH_CHECK();
+    const _Float16 *xp = static_cast<const _Float16 *>(x);
+    if (plan.nb > 2) {
+        _Float16 *copy = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kPartialOffset + plan.partial_bytes);
+        const int64_t quads = static_cast<int64_t>(plan.geo.M) * plan.geo.G * 8;  // 32-byte runs of the copy
+        hipLaunchKernelGGL(permute_activations_kernel, dim3(static_cast<unsigned>(ceil_div(quads, kThreads))),
+                           dim3(kThreads), 0, stream, static_cast<const uint2 *>(x), reinterpret_cast<uint2 *>(copy),
+                           quads, static_cast<int>(reinterpret_cast<uintptr_t>(copy) % 16 == 0));
+        TQ1_LAUNCH_CHECK();
+        xp = copy;
+    }
     WideGeometry geo = plan.geo;
     geo.vector_rows = geo.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
     switch (plan.nb) {

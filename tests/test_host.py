@@ -256,7 +256,7 @@ def test_workspace_queries() -> None:
     assert handle.ternel_tq1_gemm_workspace_bytes(65, 256, 5120, direct, 1) == 0  # rejected
     # wide form: two fp32 partial slots of 8 waves x NB fragments x 16 x 64 per
     # workgroup (one per CU, 256 without a GPU, at most one per unit), then
-    # the K-permuted fp16 copy of the activations;
+    # the K-permuted fp16 copy of the activations (four or eight blocks only);
     # NB = 1, 2, 4, 8 32-row activation blocks per tile for M <= 32, 64, 128, above,
     # and 4 instead of 8 while, with 256-wide tiles, the partials a tile's last
     # contributor reads (256/tiles - 1) exceed a tenth of the steps per CU
@@ -275,9 +275,9 @@ def test_workspace_queries() -> None:
         counters + 256 * slot_pair(8) + 1024 * 17408 * 2)
     assert handle.ternel_tq1_gemm_workspace_bytes(768, 5120, 17408, wide, 0) == (
         counters + 256 * slot_pair(4) + 768 * 17408 * 2)
-    assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 1) == counters + 5 * slot_pair(1) + 5 * 640 * 2
-    assert handle.ternel_tq1_gemm_workspace_bytes(64, 17408, 5120, wide, 0) == (
-        counters + 256 * slot_pair(2) + 64 * 5120 * 2)
+    # one or two blocks read x itself: no permuted copy
+    assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 1) == counters + 5 * slot_pair(1)
+    assert handle.ternel_tq1_gemm_workspace_bytes(64, 17408, 5120, wide, 0) == counters + 256 * slot_pair(2)
     assert handle.ternel_tq1_gemm_workspace_bytes(100, 17408, 5120, wide, 0) == (
         counters + 256 * slot_pair(4) + 100 * 5120 * 2)
     assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 2) == 0  # K is split by stream-K
