@@ -2806,44 +2806,42 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
 
 // Automatic choice, from a sweep of every form over the 27B linears on MI355X
 // (the fixture tests/golden/dispatch_sweep_mi355x.json replays it): the direct
-// form up to 32 activation rows, and up to 64 for matrices under 16 MiB of
-// packed weights (O 8192->5120 M=40-64: 26.5-28.2 us against the wide form's
-// 29.4-30.8 and the tile form's 29.4-32.7; QKV within 0.5 % of the fastest,
-// while gate/up and down stay faster on the wide form); above, the wide form
-// when stream-K has enough
-// tiles or enough work per CU to amortise its reduction -- at least CUs/4
-// tiles (a tile's partials come from at most ~4 contributors) or 15 (tile,
+// form up to 16 activation rows, and up to 32 for matrices under 16 MiB of
+// packed weights (QKV, O M=24-32: 16.3-17.7 us against the wide form's
+// 21.1-22.0); the wide form at 17-32 rows for larger matrices (gate/up, down
+// M=24-32: 24.3-27.3 us against 27.0-30.2) and at 33-64 rows for every shape
+// (QKV M=40-64: 24.3-24.9 against the direct form's 26.0-27.2, O within 3.4 %);
+// above, the wide form when stream-K has enough tiles or enough work per CU to
+// amortise its reduction -- at least CUs/4 tiles (a tile's partials come from
+// at most ~4 contributors) or 10 (one or two blocks per tile) / 15 (tile,
 // group) steps per CU -- and the fixed-split tile form otherwise (QKV
-// 5120->8192 M=128: 30.4 us against 45.8; gate/up 5120->17408 M=128: 48.7
-// against 57.7 the other way). The tile form also serves a fixed K split and
+// 5120->8192 M=128: 31.6 us against 38.8; gate/up 5120->17408 M=128: 44.6
+// against 58.1 the other way). The tile form also serves a fixed K split and
 // rows too long for the wide form's 32-bit buffer offsets.
-constexpr int64_t kAutoDirectMaxBatch = 32;
-constexpr int64_t kAutoDirectMaxBatchSmall = 64;
+constexpr int64_t kAutoDirectMaxBatch = 16;
+constexpr int64_t kAutoDirectMaxBatchSmall = 32;
+constexpr int64_t kAutoWideMaxBatch = 64;
 constexpr int64_t kAutoSmallMatrixBytes = 16ll << 20;
 int wide_blocks(int64_t M, int64_t tiles_n, int64_t groups, int64_t cus);
 int device_cu_count();
 int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (form != TERNEL_TQ1_GEMM_AUTO) return form;
-    // 17-32 rows: the wide form where one-block tiles alone number CUs/4
-    // (gate/up M=24-32: 25.4-25.6 us against the direct form's 26.4-27.1;
-    // down, QKV and O, with 20-32 such tiles, stay on the direct form).
-    if (M > 16 && M <= kAutoDirectMaxBatch && k_split <= 1 && columns <= kWideMaxColumns &&
-        4 * ceil_div(rows, kWideRows) >= device_cu_count())
-        return TERNEL_TQ1_GEMM_WIDE;
-    if (M <= kAutoDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
     const int64_t bytes = rows * (columns / kBlockWeights) * kBlockBytes;
-    if (M <= kAutoDirectMaxBatchSmall && bytes < kAutoSmallMatrixBytes) return TERNEL_TQ1_GEMM_DIRECT;
+    const bool small = bytes < kAutoSmallMatrixBytes;
+    if (M <= kAutoDirectMaxBatch || (small && M <= kAutoDirectMaxBatchSmall)) return TERNEL_TQ1_GEMM_DIRECT;
+    const bool wide_ok = k_split <= 1 && columns <= kWideMaxColumns;
+    if (M <= kAutoWideMaxBatch && wide_ok) return TERNEL_TQ1_GEMM_WIDE;
+    if (M <= kAutoDirectMaxBatchSmall) return TERNEL_TQ1_GEMM_DIRECT;  // a fixed K split at 17-32 rows
     if (k_split > 1 || columns > kWideMaxColumns) return TERNEL_TQ1_GEMM_TILE;
     const int64_t cus = device_cu_count();
     const int64_t groups = columns / kBlockWeights;
     const int64_t tiles_n = ceil_div(rows, kWideRows);
     const int nb = wide_blocks(M, tiles_n, groups, cus);
     const int64_t tiles = tiles_n * ceil_div(M, 32 * nb);
-    // Measured on MI355X: at one or two activation blocks per tile 10 (tile,
-    // group) steps per CU suffice (down M=40-64: 38.5-39.7 us against the tile
-    // form's 47.4-48.1); four or eight blocks need 15 (down M=96-128 stays on
-    // the tile form, 49.0-52.0 us against 55.5-58.5).
-    const int64_t min_steps = nb <= 2 ? 10 : 15;
+    // Measured on MI355X: above 64 rows (four or eight blocks per tile) 15
+    // (tile, group) steps per CU (down M=96-128 stays on the tile form,
+    // 49.6-52.4 us against 51.6-54.4).
+    const int64_t min_steps = 15;
     return 4 * tiles >= cus || tiles * groups >= min_steps * cus ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_TILE;
 }
 
