@@ -180,7 +180,7 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
  * accumulation, in one of three forms (the reference's GemmConfig forms,
  * src/ternel_mlx/kernels.py:1043-1188, re-chosen for CDNA4):
  *   TERNEL_TQ1_GEMM_TILE   (prefill) 128x128 output tiles, weights decoded to
- *                          fp16 (t-1)*scale tiles in LDS; x 16-byte aligned;
+ *                          fp16 (t-1)*scale tiles in LDS;
  *   TERNEL_TQ1_GEMM_DIRECT (M <= 64) weights decoded straight into MFMA
  *                          operand registers, activations staged in LDS,
  *                          split-K reduced in the same launch in chunk order;
@@ -196,8 +196,8 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
  *                          above, WIDE when it has at least CUs/4 output
  *                          tiles or 15 (tile, group) steps per CU, TILE
  *                          otherwise (and for M > 32 when k_split > 1).
- * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. k_split divides
- * columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
+ * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. x is 16-byte
+ * aligned in every form. k_split divides columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
  * same 64 KiB counter region + fp32 partials contract as ternel_tq1_matmul.
  */
 #define TERNEL_TQ1_GEMM_AUTO 0
@@ -257,7 +257,7 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
  * z is [M][rows / 2] in the activation type. No counterpart in the reference
  * (its MLP runs gate_proj, up_proj and the activation as separate mlx ops,
  * src/ternel_mlx/packed_model.py:72-92). Batches that ternel_tq1_linear sends
- * to the LUT23 kernel (up to 3 rows, 5 for matrices under 16 MiB, and every
+ * to the LUT23 kernel (up to 3 rows, 4 for matrices under 16 MiB, and every
  * bf16/fp32 batch) run it with the pair exchange in its epilogue; larger fp16
  * batches run the GEMM into the workspace and one elementwise pass. Workspace
  * from ternel_tq1_swiglu_workspace_bytes, same contract as ternel_tq1_linear's.

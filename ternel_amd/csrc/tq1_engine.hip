@@ -1393,14 +1393,16 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
         // The window's activations, staged in LDS in the K order above
         // (logical unit u of a row, 4 halves, from physical unit
         // direct_source_unit(u); rows past M re-read row M - 1). Up to 16
-        // staged rows: as 8-byte units loaded into registers (16 per thread at
-        // the window of 8 groups) ahead of the first two word sets and written
-        // to LDS after them -- loads complete in order, so the writes wait for
-        // the activations only while the words are in flight. More rows: by
+        // staged rows: as 16-byte physical chunks loaded into registers (8 per
+        // thread at the window of 8 groups) ahead of the first two word sets,
+        // each written to LDS after them as two 8-byte units at their K-order
+        // positions -- loads complete in order, so the writes wait for the
+        // activations only while the words are in flight. More rows: by
         // LDS-DMA (one padded row per instruction) waited for before any word
         // is requested, as a second register pass would wait for the words too.
         // (Measured on MI355X, gate/up: M=16 20.7 -> 19.0 us and M=8 19.2 ->
-        // 18.3 us with registers, M=32 27.8 us with LDS-DMA against 32.4.)
+        // 18.3 us with 8-byte units in registers, 17.1 us at M=8 with 16-byte
+        // chunks; M=32 27.8 us with LDS-DMA against 32.4.)
         uint32_t wa[CH][5], wb[CH][5];
         if constexpr (SR <= 16) {
             constexpr int kUnits = 16;  // per thread
@@ -1418,15 +1420,30 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
             // the last unit again, the same value): no load or write behind a
             // branch, where the compiler's wait counts turn conservative.
             const int first = min(units, kUnits * kDirectThreads);
-            uint2 xu[kUnits];
+            // 16-byte physical chunks: chunk j is row-group j / 16, physical
+            // units 2 (j % 16) and 2 (j % 16) + 1, written to their K-order
+            // positions (the inverse of direct_source_unit).
+            auto target_unit = [](int u) { return u < 15 ? u : (u < 30 ? u + 1 : (u == 30 ? 15 : 31)); };
+            const int first_chunks = first / 2;
+            uint4 xc[kUnits / 2];
 #pragma unroll
-            for (int k = 0; k < kUnits; ++k) xu[k] = *unit_source(min(tid + k * kDirectThreads, first - 1));
+            for (int k = 0; k < kUnits / 2; ++k) {
+                const int j = min(tid + k * kDirectThreads, first_chunks - 1);
+                const int r = j >> 4, q = r / SR, m = r - q * SR;
+                xc[k] = *reinterpret_cast<const uint4 *>(x + static_cast<int64_t>(min(m, M - 1)) * K +
+                                                         static_cast<int64_t>(gw + q) * kBlockWeights + (j & 15) * 8);
+            }
             __builtin_amdgcn_sched_barrier(0);
             load_chunk(wa, 0);
             load_chunk(wb, CH);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int k = 0; k < kUnits; ++k) *unit_target(min(tid + k * kDirectThreads, first - 1)) = xu[k];
+            for (int k = 0; k < kUnits / 2; ++k) {
+                const int j = min(tid + k * kDirectThreads, first_chunks - 1);
+                const int r = j >> 4, c = j & 15;
+                *reinterpret_cast<uint2 *>(xs + r * kDirectStride + target_unit(2 * c) * 4) = uint2{xc[k].x, xc[k].y};
+                *reinterpret_cast<uint2 *>(xs + r * kDirectStride + target_unit(2 * c + 1) * 4) = uint2{xc[k].z, xc[k].w};
+            }
             // (Windows of more than 8 groups at 16 rows: the rest after the words.)
             for (int i = first + tid; i < units; i += kDirectThreads) *unit_target(i) = *unit_source(i);
         } else {
@@ -2846,12 +2863,13 @@ int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_
 }
 
 // The dispatch rule of packed_matmul, retuned for MI355X by the same sweep: the
-// LUT23 kernel up to 3 activation rows -- 5 for matrices under 16 MiB of
+// LUT23 kernel up to 3 activation rows -- 4 for matrices under 16 MiB of
 // packed weights, where the MFMA forms' fixed costs weigh more (O 8192->5120
-// M=5: 13.6 us against 14.3; gate/up M=4: the direct form 17.9 us against
-// 19.3) -- the MFMA kernels above it (fp16 only).
+// M=4: 11.5 us against the direct form's 13.1, M=5 13.7 against 13.0; gate/up
+// M=4: the direct form 16.2 us against 18.9) -- the MFMA kernels above it
+// (fp16 only).
 constexpr int64_t kLinearLutMaxBatch = 3;
-constexpr int64_t kLinearLutMaxBatchSmall = 5;
+constexpr int64_t kLinearLutMaxBatchSmall = 4;
 constexpr int64_t kLinearSmallMatrixBytes = 16ll << 20;
 bool linear_uses_lut(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (dtype != TERNEL_TQ1_F16) return true;
@@ -3233,7 +3251,7 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
         if ((rc = plan_direct(M, rows, columns, k_split, &direct)) != TERNEL_TQ1_OK) return rc;
         if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
         if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
-        if (reinterpret_cast<uintptr_t>(x) & 7u) return fail(TERNEL_TQ1_EINVAL, "activations must be 8-byte aligned");
+        if (reinterpret_cast<uintptr_t>(x) & 15u) return fail(TERNEL_TQ1_EINVAL, "activations must be 16-byte aligned");
         const size_t need = direct.k_split > 1 ? kPartialOffset + direct.partial_bytes : 0;
         if (need && (!ws || ws_bytes < need))
             return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,

@@ -49,8 +49,9 @@ from .layout import PackedTensorLayout, interleave_gate_up, unpack_blocks
 # cost grows linearly with the batch (one table set per vector) while its bytes
 # do not, so it only pays while the weight stream dominates. The rule lives in
 # the library (ternel_tq1_linear_kernel, replayed against a measured sweep in
-# tests/test_dispatch.py); LUT23_MAX_BATCH is its bound for the 27B MLP shapes.
-LUT23_MAX_BATCH = 4
+# tests/test_dispatch.py); LUT23_MAX_BATCH is its bound for matrices of 16 MiB
+# of packed weights or more, the 27B MLP shapes (smaller matrices: 4 rows).
+LUT23_MAX_BATCH = 3
 _KERNEL_NAMES = {100: "lut23", 1: "gemm", 2: "gemm", 3: "gemm"}
 
 

@@ -133,8 +133,8 @@ def test_packed_linear_matches_the_oracle_in_every_dispatch_regime(batch: int) -
     got = module(to_dev(x)).float().cpu().numpy()
     oracle = O.oracle_matmul(blocks, x.astype(np.float64), rows=512, columns=640)
     assert O.compare(got, oracle)["normalised_max_abs_error"] < 1e-3
-    # 512 x 640 is under 16 MiB of packed weights: LUT23 up to 5 activation rows
-    assert select_kernel(module.layout, batch, torch.float16) == ("lut23" if batch <= 5 else "gemm")
+    # 512 x 640 is under 16 MiB of packed weights: LUT23 up to 4 activation rows
+    assert select_kernel(module.layout, batch, torch.float16) == ("lut23" if batch <= 4 else "gemm")
 
 
 def test_packed_linear_keeps_leading_dimensions() -> None:

@@ -186,6 +186,11 @@ def test_argument_errors_are_reported_without_a_launch() -> None:
     assert rc == _lib.TERNEL_TQ1_EINVAL and "unknown GEMM form 7" in _lib.last_error()
     rc = handle.ternel_tq1_gemm(None, None, None, 65, 256, 5120, 0, 2, 0, None, 0, None)
     assert rc == _lib.TERNEL_TQ1_EINVAL and "at most 64 activation rows" in _lib.last_error()
+    # every GEMM form loads activations 16 bytes at a time
+    for form, M, k_split in ((1, 40, 1), (2, 8, 1), (3, 40, 0)):
+        rc = handle.ternel_tq1_gemm(ctypes.c_void_p(4096), ctypes.c_void_p(4104), ctypes.c_void_p(8192), M, 256, 5120,
+                                    0, form, k_split, None, 0, None)
+        assert rc == _lib.TERNEL_TQ1_EINVAL and "16-byte aligned" in _lib.last_error()
     rc = handle.ternel_tq1_get_rows(None, 256, 5120, None, 0, None, 0, None)
     assert rc == _lib.TERNEL_TQ1_EINVAL and "indices are empty" in _lib.last_error()
     rc = handle.ternel_tq1_get_rows_canonical(ctypes.c_void_p(4098), 256, 5120, None, 1, None, 0, None)
