@@ -74,6 +74,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--traffic-probe", action="store_true",
                    help="only launch the dominant kernel eagerly over the cold ring, then a plain copy of "
                         "COPY_BYTES, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    p.add_argument("--dense-reference", action="store_true",
+                   help="time the dense fp16 product of the same shapes through torch.mm (the vendor BLAS) at "
+                        "M = 1, 16, 512 and 2048, for comparison with the packed kernels, one JSON line each")
     p.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                    help="summarise a rocprofv3 kernel_trace.csv per (kernel, grid) and exit")
     return p.parse_args()
@@ -266,6 +269,8 @@ def main() -> int:
 
     if args.stream_ceiling:
         return stream_ceiling(torch, dev, graph_of, time_graph)
+    if args.dense_reference:
+        return dense_reference(torch, dev, graph_of, time_graph)
     if args.phase_profile:
         return phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_linear_words,
                              PackedTensorLayout, MatmulConfig, graph_of, time_graph, args.phase_batch)
@@ -570,6 +575,51 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
             "clock": "s_memrealtime (100 MHz), lane 0 of every wave, grouped by HW_REG_XCC_ID, 3 cold launches"}),
             flush=True)
         del weights
+    return 0
+
+
+DENSE_BATCHES = (1, 16, 512, 2048)
+
+
+def dense_reference(torch, dev, graph_of, time_graph) -> int:
+    """The same products with dense fp16 weights through torch.mm (hipBLASLt / rocBLAS):
+    what a vendor-library GEMM of the unpacked matrix costs on this GPU. y = x @ Wt with
+    Wt a contiguous (K, N) fp16 matrix (2 bytes per weight against the packed 0.219).
+    Batches up to 16 rotate over a ring of distinct weight copies (cold, HBM-bound);
+    512 and 2048 reuse one copy (MFMA-bound, the weight read is 3-10 % of the time).
+    Eager launches back to back between one event pair (a library call is not put into
+    a graph here: it may record memset nodes)."""
+    del graph_of, time_graph
+
+    def timed(fn, launches: int) -> float:
+        fn(0)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for s in range(launches):
+            fn(s)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / launches * 1e3
+
+    for name, K, N in C1_SHAPES:
+        dense_bytes = K * N * 2
+        ring = max(2, -(-RING_BYTES_MIN // dense_bytes))
+        gen = torch.Generator(device=dev).manual_seed(2024)
+        weights = [(torch.randn(K, N, device=dev, generator=gen) * 0.02).half() for _ in range(ring)]
+        for M in DENSE_BATCHES:
+            x = torch.randn(M, K, device=dev, generator=gen).half()
+            copies = ring if M <= 16 else 1
+            launches = ring * 4 if M <= 16 else 20
+            us = sorted(timed(lambda s: torch.mm(x, weights[s % copies]), launches) for _ in range(3))[1]
+            flops = 2.0 * M * K * N
+            print(json.dumps({"dense_reference": name, "K": K, "N": N, "M": M, "dtype": "f16",
+                              "weights": "cold ring" if copies > 1 else "one copy", "us": round(us, 2),
+                              "TFLOP/s": round(flops / us / 1e6, 1),
+                              "weight_GB/s": round(dense_bytes / us / 1e3, 1),
+                              "packed_bytes": packed_bytes(K, N), "dense_bytes": dense_bytes}), flush=True)
+        del weights
+        torch.cuda.empty_cache()
     return 0
 
 
