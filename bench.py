@@ -14,7 +14,8 @@ kernel (the gate/up GEMV): packed bytes per launch / its average launch
 duration, from HIP events on the launch stream around `steps` cold launches
 replayed back to back from one graph; ``traffic`` is the HBM bytes per launch
 from the calibrated rocprofv3 --pmc passes recorded under profiles/. Secondary
-figures: the small-batch GEMM (configs[2], M=2..64, GB/s), the prefill GEMM
+figures: the 4096 x 4096 GEMV (configs[0], cold and warm), the small-batch GEMM
+(configs[2], M=2..64, GB/s), the prefill GEMM
 (configs[3], M=512 and 2048, TFLOP/s against the fp16 MFMA peak), the 64-layer
 weight stream with one embedding row, and the reference's CPU
 decode+matmul path (the oracle restatement) timed on the host cores on a
@@ -35,6 +36,7 @@ import time
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 
+C0_K = C0_N = 4096  # configs[0]
 C1_SHAPES = (("gate_up", 5120, 17408), ("down", 17408, 5120), ("qkv", 5120, 8192))  # (name, K, N)
 C3_SHAPES = (("gate_up", 5120, 17408), ("down", 17408, 5120))
 SMALL_BATCHES = (2, 4, 8, 16, 32, 64)
@@ -137,7 +139,7 @@ def cpu_baseline(seconds: float) -> dict:
     mm_calls, mm_elapsed = timed_calls(lambda: O.cpu_matmul(dense, x), 0.15 * seconds)
     del dense, blocks
 
-    K0 = N0 = 4096
+    K0, N0 = C0_K, C0_N
     blocks0 = synthetic.host_blocks(N0, K0, seed=synthetic.SEED_BASE + 0)
     x0 = synthetic.host_activations(1, K0, seed=synthetic.SEED_BASE + 0)
     c0_calls, c0_elapsed = timed_calls(lambda: O.cpu_decode_matmul(blocks0, x0, rows=N0, columns=K0), 0.15 * seconds)
@@ -365,6 +367,27 @@ def main() -> int:
     warm_ms = time_graph(warm) / 100
     del warm
 
+    # ---- config 0: 4096 x 4096 at M=1, cold (a ring of distinct copies) and warm --
+    c0_layout = PackedTensorLayout.for_tensor(C0_N, C0_K)
+    c0_bytes = packed_bytes(C0_K, C0_N)
+    c0_first = pack_weights(synthetic.device_blocks(C0_N, C0_K, seed=synthetic.SEED_BASE), layout=c0_layout)
+    c0_ring = max(2, -(-RING_BYTES_MIN // c0_bytes))
+    c0_weights = [c0_first] + [c0_first.clone() for _ in range(c0_ring - 1)]
+    c0_x = synthetic.device_activations(1, C0_K, seed=synthetic.SEED_BASE)
+    config0 = {"workload": "BASELINE configs[0]: M=1, K=N=4096, fp16 activations, LUT23 GEMV",
+               "packed_bytes": c0_bytes, "kernel": select_kernel(c0_layout, 1, torch.float16)}
+    for label, copies in (("cold", c0_ring), ("warm", 1)):
+        launches = max(c0_ring, 200)
+        g = graph_of(lambda copies=copies: [tq1_matmul_words(c0_weights[s % copies], c0_x, layout=c0_layout,
+                                                             config=config) for s in range(launches)])
+        ms = time_graph(g, 3) / 3 / launches
+        del g
+        config0[label] = {"us": round(ms * 1e3, 3), "GB/s": round(c0_bytes / (ms * 1e-3) / 1e9, 1),
+                          "copies": copies}
+    config0["cold"]["note"] = f"{c0_ring} distinct copies ({c0_ring * c0_bytes >> 20} MiB) in rotation"
+    config0["warm"]["note"] = "one copy, MALL/L2-resident after the first launch"
+    del c0_weights, c0_first
+
     # ---- config 2: small batches over the same cold ring (library dispatch) ------
     small_batch = {}
     if not args.no_small_batch:
@@ -408,6 +431,7 @@ def main() -> int:
         },
         "per_matrix": per_matrix,
         "warm_gate_up_GBs": round(dom_bytes / (warm_ms * 1e-3) / 1e9, 1),
+        "config0": config0,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
