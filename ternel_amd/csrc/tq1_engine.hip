@@ -1393,18 +1393,21 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
         // The window's activations, staged in LDS in the K order above
         // (logical unit u of a row, 4 halves, from physical unit
         // direct_source_unit(u); rows past M re-read row M - 1). Up to 16
-        // staged rows: as 16-byte physical chunks loaded into registers (8 per
-        // thread at the window of 8 groups) ahead of the first two word sets,
-        // each written to LDS after them as two 8-byte units at their K-order
-        // positions -- loads complete in order, so the writes wait for the
-        // activations only while the words are in flight. More rows: by
-        // LDS-DMA (one padded row per instruction) waited for before any word
-        // is requested, as a second register pass would wait for the words too.
-        // (Measured on MI355X, gate/up: M=16 20.7 -> 19.0 us and M=8 19.2 ->
-        // 18.3 us with 8-byte units in registers, 17.1 us at M=8 with 16-byte
-        // chunks; M=32 27.8 us with LDS-DMA against 32.4.)
+        // staged rows, and 32 rows in windows of up to 4 groups (the planner's
+        // window there): as 16-byte physical chunks loaded into registers (8
+        // per thread at 16 rows x 8 groups or 32 rows x 4) ahead of the first
+        // two word sets, each written to LDS after them as two 8-byte units at
+        // their K-order positions -- loads complete in order, so the writes
+        // wait for the activations only while the words are in flight.
+        // Otherwise by LDS-DMA (one padded row per instruction) waited for
+        // before any word is requested, as a second register pass would wait
+        // for the words too. (Measured on MI355X, gate/up: M=16 20.7 -> 19.0
+        // us and M=8 19.2 -> 18.3 us with 8-byte units in registers, 17.1 us
+        // at M=8 with 16-byte chunks; M=32 in 8-group windows 27.8 us with
+        // LDS-DMA against 32.4 with registers, 20.3 us in 4-group windows with
+        // registers.)
         uint32_t wa[CH][5], wb[CH][5];
-        if constexpr (SR <= 16) {
+        if (SR <= 16 || (SR == 32 && wn * SR * 16 <= 8 * kDirectThreads)) {
             constexpr int kUnits = 16;  // per thread
             const int units = wn * SR * 32;
             auto unit_source = [&](int i) {
@@ -2641,12 +2644,12 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
     if (k_split == 0) {
         // Measured on MI355X: chunks of a multiple of 8 groups keep the whole
         // K chunk in the 8-step pipeline; take the smallest such split that
-        // reaches the workgroup target, else the largest such split. At the
-        // 32-row window (two workgroups per CU) chunks of a multiple of 4
-        // qualify too, whose last four groups run the same pipeline: QKV and O
-        // at M=32 then run 640 workgroups instead of 320 (16.9 and 17.2 us
-        // against 18.4 and 18.3); at up to 16 rows 4-group chunks measured
-        // slower.
+        // reaches the workgroup target, else the largest such split. At 32
+        // staged rows chunks of a multiple of 4 qualify too, whose last four
+        // groups run the same pipeline (QKV and O at M=32 then run 640
+        // workgroups instead of 320: 16.9 and 17.2 us against 18.4 and 18.3,
+        // measured with 8-group windows); at up to 16 rows 4-group chunks
+        // measured slower.
         const int64_t granule = plan->staged_rows == 32 ? 4 : 8;
         int best = 0;
         for (int64_t k = 1; k <= G; ++k) {
@@ -2671,6 +2674,11 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
     // fit a CU's LDS (69.6 KiB each, against one at 8 groups); measured on
     // MI355X, gate/up M=40 38.4 us against 53.0, QKV 24.9 against 35.7.
     if (plan->nb == 2 && window > 4) window = 4;
+    // 32 staged rows: windows of 4 groups too (34.8 KiB: three workgroups per
+    // CU, and the activations fit the register staging); measured on MI355X
+    // at M=17-32, gate/up 19.2-20.7 us against 26.2-26.9 in 8-group windows,
+    // down 20.7-22.5 against 27.5-28.8, QKV and O 13.7-15.5 against 15.3-17.1.
+    if (plan->staged_rows == 32 && window > 4) window = 4;
     if (window >= plan->chunk_groups)
         window = plan->chunk_groups;
     else if (window >= 8)
@@ -2823,32 +2831,25 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
 
 // Automatic choice, from a sweep of every form over the 27B linears on MI355X
 // (the fixture tests/golden/dispatch_sweep_mi355x.json replays it): the direct
-// form up to 16 activation rows, and up to 32 for matrices under 16 MiB of
-// packed weights (QKV, O M=24-32: 16.3-17.7 us against the wide form's
-// 21.1-22.0); the wide form at 17-32 rows for larger matrices (gate/up, down
-// M=24-32: 24.3-27.3 us against 27.0-30.2) and at 33-64 rows for every shape
-// (QKV M=40-64: 24.3-24.9 against the direct form's 26.0-27.2, O within 3.4 %);
-// above, the wide form when stream-K has enough tiles or enough work per CU to
-// amortise its reduction -- at least CUs/4 tiles (a tile's partials come from
-// at most ~4 contributors) or 10 (one or two blocks per tile) / 15 (tile,
-// group) steps per CU -- and the fixed-split tile form otherwise (QKV
-// 5120->8192 M=128: 31.6 us against 38.8; gate/up 5120->17408 M=128: 44.6
-// against 58.1 the other way). The tile form also serves a fixed K split and
-// rows too long for the wide form's 32-bit buffer offsets.
-constexpr int64_t kAutoDirectMaxBatch = 16;
-constexpr int64_t kAutoDirectMaxBatchSmall = 32;
+// form up to 32 activation rows (gate/up, down M=24-32: 19.9-23.1 us against
+// the wide form's 24.0-27.2; QKV, O 14.9-16.3 against 20.9-21.5); the wide
+// form at 33-64 rows (gate/up, down M=40-64: 29.1-33.5 against the two-tile
+// direct form's 38.0-44.1; QKV, O within 2 %); above, the wide form when
+// stream-K has enough tiles or enough work per CU to amortise its reduction --
+// at least CUs/4 tiles (a tile's partials come from at most ~4 contributors)
+// or 15 (tile, group) steps per CU -- and the fixed-split tile form otherwise
+// (QKV 5120->8192 M=128: 31.6 us against 38.8; gate/up 5120->17408 M=128: 44.6
+// against 58.1 the other way). The tile form also serves a fixed K split above
+// 32 rows and rows too long for the wide form's 32-bit buffer offsets.
+constexpr int64_t kAutoDirectMaxBatch = 32;
 constexpr int64_t kAutoWideMaxBatch = 64;
-constexpr int64_t kAutoSmallMatrixBytes = 16ll << 20;
 int wide_blocks(int64_t M, int64_t tiles_n, int64_t groups, int64_t cus);
 int device_cu_count();
 int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (form != TERNEL_TQ1_GEMM_AUTO) return form;
-    const int64_t bytes = rows * (columns / kBlockWeights) * kBlockBytes;
-    const bool small = bytes < kAutoSmallMatrixBytes;
-    if (M <= kAutoDirectMaxBatch || (small && M <= kAutoDirectMaxBatchSmall)) return TERNEL_TQ1_GEMM_DIRECT;
+    if (M <= kAutoDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
     const bool wide_ok = k_split <= 1 && columns <= kWideMaxColumns;
     if (M <= kAutoWideMaxBatch && wide_ok) return TERNEL_TQ1_GEMM_WIDE;
-    if (M <= kAutoDirectMaxBatchSmall) return TERNEL_TQ1_GEMM_DIRECT;  // a fixed K split at 17-32 rows
     if (k_split > 1 || columns > kWideMaxColumns) return TERNEL_TQ1_GEMM_TILE;
     const int64_t cus = device_cu_count();
     const int64_t groups = columns / kBlockWeights;
