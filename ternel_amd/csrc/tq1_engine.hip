@@ -1328,11 +1328,12 @@ __device__ __forceinline__ void direct_mfma(float16v (&acc)[NB], const uint32_t 
 // direct_source_unit(u) of the group (the K order above).
 __device__ __forceinline__ int direct_source_unit(int u) { return u < 15 ? u : (u == 15 ? 30 : (u < 31 ? u - 1 : 31)); }
 
-// Three waves per SIMD for one activation tile: a CU then holds three
-// workgroups, so the grid (about 2.7 workgroups per CU at the 27B shapes)
-// runs in one round.
+// Three waves per SIMD (168 VGPRs at most; the two-tile form keeps one 8-byte
+// value in scratch, reloaded once per eight-group loop pass): a CU then holds
+// three workgroups, so the grid (about 2.7 workgroups per CU at the 27B
+// shapes) runs in one round.
 template <int NB, int SR>
-__global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_kernel(
+__global__ __launch_bounds__(kDirectThreads, 3) void direct_gemm_kernel(
     const uint32_t *__restrict__ packed, const _Float16 *__restrict__ x, _Float16 *__restrict__ y,
     float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
     int k_split, int window) {
@@ -1393,9 +1394,10 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
         // The window's activations, staged in LDS in the K order above
         // (logical unit u of a row, 4 halves, from physical unit
         // direct_source_unit(u); rows past M re-read row M - 1). Up to 16
-        // staged rows, and 32 rows in windows of up to 4 groups (the planner's
-        // window there): as 16-byte physical chunks loaded into registers (8
-        // per thread at 16 rows x 8 groups or 32 rows x 4) ahead of the first
+        // staged rows, 32 rows in windows of up to 4 groups and 64 in windows
+        // of up to 2 (the planner's windows there): as 16-byte physical chunks
+        // loaded into registers (8 per thread at 16 rows x 8 groups, 32 x 4 or
+        // 64 x 2) ahead of the first
         // two word sets, each written to LDS after them as two 8-byte units at
         // their K-order positions -- loads complete in order, so the writes
         // wait for the activations only while the words are in flight.
@@ -1407,7 +1409,7 @@ __global__ __launch_bounds__(kDirectThreads, NB == 1 ? 3 : 2) void direct_gemm_k
         // LDS-DMA against 32.4 with registers, 20.3 us in 4-group windows with
         // registers.)
         uint32_t wa[CH][5], wb[CH][5];
-        if (SR <= 16 || (SR == 32 && wn * SR * 16 <= 8 * kDirectThreads)) {
+        if (SR <= 16 || wn * SR * 16 <= 8 * kDirectThreads) {
             constexpr int kUnits = 16;  // per thread
             const int units = wn * SR * 32;
             auto unit_source = [&](int i) {
@@ -2670,15 +2672,16 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
     plan->chunk_groups = static_cast<int>(G / k_split);
     const size_t group_bytes = static_cast<size_t>(plan->staged_rows) * kDirectStride * sizeof(_Float16);
     int window = static_cast<int>(kDirectLdsBytes / group_bytes);
-    // Two tiles (64 staged rows): windows of 4 groups, so that two workgroups
-    // fit a CU's LDS (69.6 KiB each, against one at 8 groups); measured on
-    // MI355X, gate/up M=40 38.4 us against 53.0, QKV 24.9 against 35.7.
-    if (plan->nb == 2 && window > 4) window = 4;
-    // 32 staged rows: windows of 4 groups too (34.8 KiB: three workgroups per
-    // CU, and the activations fit the register staging); measured on MI355X
-    // at M=17-32, gate/up 19.2-20.7 us against 26.2-26.9 in 8-group windows,
-    // down 20.7-22.5 against 27.5-28.8, QKV and O 13.7-15.5 against 15.3-17.1.
+    // Windows of 34.8 KiB of activations: three workgroups per CU, and the
+    // window fits the register staging. 32 staged rows: 4 groups, measured on
+    // MI355X at M=17-32 gate/up 19.2-20.7 us against 26.2-26.9 in 8-group
+    // windows, down 20.7-22.5 against 27.5-28.8, QKV and O 13.7-15.5 against
+    // 15.3-17.1. Two tiles (64 staged rows): 2 groups, at M=40-64 gate/up
+    // 31.6-32.8 us against 38.2-39.5 in 4-group windows with two workgroups
+    // per CU (and 53.0 at M=40 in 8-group windows, one per CU), down
+    // 33.7-35.5 against 40.7-43.1, QKV and O 23.2-25.9 against 24.9-27.2.
     if (plan->staged_rows == 32 && window > 4) window = 4;
+    if (plan->nb == 2 && window > 2) window = 2;
     if (window >= plan->chunk_groups)
         window = plan->chunk_groups;
     else if (window >= 8)
@@ -2831,10 +2834,10 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
 
 // Automatic choice, from a sweep of every form over the 27B linears on MI355X
 // (the fixture tests/golden/dispatch_sweep_mi355x.json replays it): the direct
-// form up to 32 activation rows (gate/up, down M=24-32: 19.9-23.1 us against
-// the wide form's 24.0-27.2; QKV, O 14.9-16.3 against 20.9-21.5); the wide
-// form at 33-64 rows (gate/up, down M=40-64: 29.1-33.5 against the two-tile
-// direct form's 38.0-44.1; QKV, O within 2 %); above, the wide form when
+// form up to 32 activation rows (gate/up, down M=24-32: 19.9-23.6 us against
+// the wide form's 24.1-28.0; QKV, O 15.0-16.3 against 20.8-21.5); the wide
+// form at 33-64 rows (gate/up, down M=40-64: 29.0-34.1 against the two-tile
+// direct form's 31.8-37.8; QKV, O within 6 %); above, the wide form when
 // stream-K has enough tiles or enough work per CU to amortise its reduction --
 // at least CUs/4 tiles (a tile's partials come from at most ~4 contributors)
 // or 15 (tile, group) steps per CU -- and the fixed-split tile form otherwise
