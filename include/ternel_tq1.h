@@ -191,10 +191,11 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
  *                          LDS, K split stream-K over one workgroup per CU
  *                          with an ordered in-launch reduction (k_split must
  *                          be 0/1; columns < 2^22);
- *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 32; WIDE up to M = 64; above,
- *                          WIDE when it has at least CUs/4 output tiles or
- *                          15 (tile, group) steps per CU, TILE otherwise
- *                          (and for M > 32 when k_split > 1).
+ *   TERNEL_TQ1_GEMM_AUTO   DIRECT for M <= 32 (M <= 48 for matrices under
+ *                          16 MiB of packed weights); WIDE up to M = 64;
+ *                          above, WIDE when it has at least CUs/4 output
+ *                          tiles or 15 (tile, group) steps per CU, TILE
+ *                          otherwise (and for a fixed k_split > 1).
  * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. x is 16-byte
  * aligned in every form. k_split divides columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
  * same 64 KiB counter region + fp32 partials contract as ternel_tq1_matmul.

@@ -2647,12 +2647,13 @@ int plan_direct(int64_t M, int64_t rows, int64_t columns, int k_split, DirectPla
         // Measured on MI355X: chunks of a multiple of 8 groups keep the whole
         // K chunk in the 8-step pipeline; take the smallest such split that
         // reaches the workgroup target, else the largest such split. At 32
-        // staged rows chunks of a multiple of 4 qualify too, whose last four
-        // groups run the same pipeline (QKV and O at M=32 then run 640
+        // and 64 staged rows chunks of a multiple of 4 qualify too, whose last
+        // four groups run the same pipeline (QKV and O at M=32 then run 640
         // workgroups instead of 320: 16.9 and 17.2 us against 18.4 and 18.3,
-        // measured with 8-group windows); at up to 16 rows 4-group chunks
-        // measured slower.
-        const int64_t granule = plan->staged_rows == 32 ? 4 : 8;
+        // measured with 8-group windows; at M=40-64 QKV 20.7-22.6 us against
+        // 23.2-25.2, O 22.8-24.8 against 24.1-26.0); at up to 16 rows 4-group
+        // chunks measured slower.
+        const int64_t granule = plan->staged_rows >= 32 ? 4 : 8;
         int best = 0;
         for (int64_t k = 1; k <= G; ++k) {
             if (G % k || (G / k) % granule) continue;
@@ -2835,9 +2836,11 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
 // Automatic choice, from a sweep of every form over the 27B linears on MI355X
 // (the fixture tests/golden/dispatch_sweep_mi355x.json replays it): the direct
 // form up to 32 activation rows (gate/up, down M=24-32: 19.9-23.6 us against
-// the wide form's 24.1-28.0; QKV, O 15.0-16.3 against 20.8-21.5); the wide
-// form at 33-64 rows (gate/up, down M=40-64: 29.0-34.1 against the two-tile
-// direct form's 31.8-37.8; QKV, O within 6 %); above, the wide form when
+// the wide form's 24.1-28.0; QKV, O 15.0-16.3 against 20.8-21.5), and up to
+// 48 for matrices under 16 MiB of packed weights (QKV M=40-48: 22.2-23.0
+// against 24.3-24.5; O 25.2-27.0 against 27.0-27.3); the wide form otherwise
+// up to 64 rows (gate/up, down M=40-64: 28.9-33.6 against the two-tile direct
+// form's 31.2-37.5; QKV and O at M=64 within 5 %); above, the wide form when
 // stream-K has enough tiles or enough work per CU to amortise its reduction --
 // at least CUs/4 tiles (a tile's partials come from at most ~4 contributors)
 // or 15 (tile, group) steps per CU -- and the fixed-split tile form otherwise
@@ -2845,12 +2848,15 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
 // against 58.1 the other way). The tile form also serves a fixed K split above
 // 32 rows and rows too long for the wide form's 32-bit buffer offsets.
 constexpr int64_t kAutoDirectMaxBatch = 32;
+constexpr int64_t kAutoDirectMaxBatchSmall = 48;
+constexpr int64_t kAutoSmallMatrixBytes = 16ll << 20;
 constexpr int64_t kAutoWideMaxBatch = 64;
 int wide_blocks(int64_t M, int64_t tiles_n, int64_t groups, int64_t cus);
 int device_cu_count();
 int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_split) {
     if (form != TERNEL_TQ1_GEMM_AUTO) return form;
-    if (M <= kAutoDirectMaxBatch) return TERNEL_TQ1_GEMM_DIRECT;
+    const bool small = rows * (columns / kBlockWeights) * kBlockBytes < kAutoSmallMatrixBytes;
+    if (M <= kAutoDirectMaxBatch || (small && M <= kAutoDirectMaxBatchSmall)) return TERNEL_TQ1_GEMM_DIRECT;
     const bool wide_ok = k_split <= 1 && columns <= kWideMaxColumns;
     if (M <= kAutoWideMaxBatch && wide_ok) return TERNEL_TQ1_GEMM_WIDE;
     if (k_split > 1 || columns > kWideMaxColumns) return TERNEL_TQ1_GEMM_TILE;

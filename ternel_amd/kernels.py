@@ -96,8 +96,8 @@ class GemmConfig:
     decodes straight into MFMA operand registers (at most 64 activation rows),
     ``"wide"`` decodes into the operand registers of 256-row output tiles (32
     to 256 activation rows wide) split stream-K over the CUs (prefill; K split
-    0 or 1), ``"auto"`` takes ``"direct"`` up to 32 rows, ``"wide"`` up to 64
-    and, above, ``"wide"`` when
+    0 or 1), ``"auto"`` takes ``"direct"`` up to 32 rows (48 for matrices under
+    16 MiB of packed weights), ``"wide"`` up to 64 and, above, ``"wide"`` when
     it has enough tiles (CUs/4) or work per CU (15 steps) for its stream-K
     reduction to pay, ``"tile"`` otherwise (and, above 32 rows, whenever a K
     split above 1 is fixed).
