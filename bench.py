@@ -42,6 +42,12 @@ C3_SHAPES = (("gate_up", 5120, 17408), ("down", 17408, 5120))
 SMALL_BATCHES = (2, 4, 8, 16, 32, 64)
 PREFILL_BATCHES = (512, 2048)
 RING_BYTES_MIN = 600 * 1024 * 1024  # > 2 x (256 MiB MALL + L2)
+RING_COPIES_MIN = 16                # and at least this many distinct copies
+
+
+def ring_copies(matrix_bytes: int) -> int:
+    """Distinct copies a cold ring of one matrix needs."""
+    return max(RING_COPIES_MIN, -(-RING_BYTES_MIN // matrix_bytes))
 
 
 def packed_bytes(K: int, N: int) -> int:
@@ -293,16 +299,20 @@ def main() -> int:
 
     # ---- config 1: ring of distinct weight copies, cold ----------------------------
     step_bytes = sum(packed_bytes(K, N) for _, K, N in C1_SHAPES)
-    ring = max(2, -(-RING_BYTES_MIN // step_bytes))
+    # One ring per matrix, each at least RING_BYTES_MIN and RING_COPIES_MIN
+    # distinct copies: every cell that rotates one matrix reads it cold.
+    rings = [ring_copies(packed_bytes(K, N)) for _, K, N in C1_SHAPES]
+    ring_bytes = [r * packed_bytes(K, N) for r, (_, K, N) in zip(rings, C1_SHAPES)]
     layouts = [PackedTensorLayout.for_tensor(N, K) for _, K, N in C1_SHAPES]
     weights = [[pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
-                for i, ((_, K, N), lay) in enumerate(zip(C1_SHAPES, layouts))] for r in range(ring)]
+                for r in range(ring)] for i, ((_, K, N), lay, ring) in enumerate(zip(C1_SHAPES, layouts, rings))]
+    ring = max(rings)  # steps of the three-matrix loop before every matrix has cycled its ring
     xs = [synthetic.device_activations(1, K, seed=synthetic.SEED_BASE + 1 + i) for i, (_, K, _) in enumerate(C1_SHAPES)]
     config = MatmulConfig()
 
     def step(r: int) -> None:
         for i, lay in enumerate(layouts):
-            tq1_matmul_words(weights[r][i], xs[i], layout=lay, config=config)
+            tq1_matmul_words(weights[i][r % rings[i]], xs[i], layout=lay, config=config)
 
     for w in range(args.warmup):
         step(w % ring)
@@ -314,7 +324,7 @@ def main() -> int:
         xt = xs[0] if args.traffic_batch == 1 else synthetic.device_activations(
             args.traffic_batch, C1_SHAPES[0][1], seed=synthetic.SEED_BASE + 1)
         for s in range(args.steps):
-            tq1_linear_words(weights[s % ring][0], xt, layout=layouts[0])
+            tq1_linear_words(weights[0][s % rings[0]], xt, layout=layouts[0])
         src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(args.steps):
@@ -337,7 +347,7 @@ def main() -> int:
     dominant = 0
     dom_name, dom_K, dom_N = C1_SHAPES[dominant]
     dom_bytes = packed_bytes(dom_K, dom_N)
-    dom_graph = graph_of(lambda: [tq1_matmul_words(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant],
+    dom_graph = graph_of(lambda: [tq1_matmul_words(weights[dominant][s % rings[dominant]], xs[dominant], layout=layouts[dominant],
                                              config=config) for s in range(args.steps)])
     graph_launch_ms = time_graph(dom_graph) / args.steps
     del dom_graph
@@ -347,7 +357,7 @@ def main() -> int:
     pairs = [events() for _ in range(args.steps)]
     for s in range(args.steps):
         pairs[s][0].record(stream)
-        tq1_matmul_words(weights[s % ring][dominant], xs[dominant], layout=layouts[dominant], config=config)
+        tq1_matmul_words(weights[dominant][s % rings[dominant]], xs[dominant], layout=layouts[dominant], config=config)
         pairs[s][1].record(stream)
     torch.cuda.synchronize()
     launch_ms = sorted(a.elapsed_time(b) for a, b in pairs)
@@ -357,12 +367,13 @@ def main() -> int:
         return launch_ms[min(len(launch_ms) - 1, int(round(q * (len(launch_ms) - 1))))]
     per_matrix = {}
     for i, (name, K, N) in enumerate(C1_SHAPES):
-        g = graph_of(lambda i=i: [tq1_matmul_words(weights[s % ring][i], xs[i], layout=layouts[i], config=config)
-                                  for s in range(ring * 4)])
-        ms = sorted(time_graph(g) for _ in range(3))[1] / (ring * 4)  # median of three replays
-        per_matrix[name] = {"graph_ms_per_launch": round(ms, 5), "GB/s": round(packed_bytes(K, N) / (ms * 1e-3) / 1e9, 1)}
+        g = graph_of(lambda i=i: [tq1_matmul_words(weights[i][s % rings[i]], xs[i], layout=layouts[i], config=config)
+                                  for s in range(rings[i] * 4)])
+        ms = sorted(time_graph(g) for _ in range(3))[1] / (rings[i] * 4)  # median of three replays
+        per_matrix[name] = {"graph_ms_per_launch": round(ms, 5), "GB/s": round(packed_bytes(K, N) / (ms * 1e-3) / 1e9, 1),
+                            "ring_copies": rings[i], "ring_MiB": round(ring_bytes[i] / 2**20)}
         del g
-    warm = graph_of(lambda: [tq1_matmul_words(weights[0][dominant], xs[dominant], layout=layouts[dominant], config=config)
+    warm = graph_of(lambda: [tq1_matmul_words(weights[dominant][0], xs[dominant], layout=layouts[dominant], config=config)
                              for _ in range(100)])
     warm_ms = time_graph(warm) / 100
     del warm
@@ -371,7 +382,7 @@ def main() -> int:
     c0_layout = PackedTensorLayout.for_tensor(C0_N, C0_K)
     c0_bytes = packed_bytes(C0_K, C0_N)
     c0_first = pack_weights(synthetic.device_blocks(C0_N, C0_K, seed=synthetic.SEED_BASE), layout=c0_layout)
-    c0_ring = max(2, -(-RING_BYTES_MIN // c0_bytes))
+    c0_ring = ring_copies(c0_bytes)
     c0_weights = [c0_first] + [c0_first.clone() for _ in range(c0_ring - 1)]
     c0_x = synthetic.device_activations(1, C0_K, seed=synthetic.SEED_BASE)
     config0 = {"workload": "BASELINE configs[0]: M=1, K=N=4096, fp16 activations, LUT23 GEMV",
@@ -395,9 +406,9 @@ def main() -> int:
             xm = [synthetic.device_activations(M, K, seed=synthetic.SEED_BASE + 2 + M) for _, K, _ in C1_SHAPES]
             row = {}
             for i, (name, K, N) in enumerate(C1_SHAPES):
-                g = graph_of(lambda i=i: [tq1_linear_words(weights[s % ring][i], xm[i], layout=layouts[i])
-                                          for s in range(ring * 2)])
-                ms = sorted(time_graph(g) for _ in range(3))[1] / (ring * 2)  # median of three replays
+                g = graph_of(lambda i=i: [tq1_linear_words(weights[i][s % rings[i]], xm[i], layout=layouts[i])
+                                          for s in range(rings[i] * 2)])
+                ms = sorted(time_graph(g) for _ in range(3))[1] / (rings[i] * 2)  # median of three replays
                 del g
                 row[name] = {"us": round(ms * 1e3, 2),
                              "GB/s": round(packed_bytes(K, N) / (ms * 1e-3) / 1e9, 1),
@@ -420,8 +431,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "activation_dtype": "f16",
-        "data": "synthetic (BASELINE trit/scale/activation distributions; cold ring of "
-                f"{ring} distinct weight copies, {ring * step_bytes / 2**20:.0f} MiB); steps replayed from a HIP graph",
+        "data": "synthetic (BASELINE trit/scale/activation distributions; one cold ring per matrix of "
+                f"{'/'.join(str(r) for r in rings)} distinct copies, "
+                f"{'/'.join(str(round(b / 2**20)) for b in ring_bytes)} MiB); steps replayed from a HIP graph",
         "config": {
             "workload": "BASELINE configs[1]: M=1 GEMV over gate/up 5120->17408, down 17408->5120, "
                         "QKV 5120->8192 (one step = the three GEMVs)",
@@ -533,7 +545,6 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
     max_waves = 8192
     slots = 16  # the phases, then (last slot) 1 + the XCC id
     buf = (ctypes.c_ulonglong * (max_waves * slots))()
-    ring = 14
 
     def quantiles(values: list) -> dict:
         values = sorted(values)
@@ -544,6 +555,7 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
         wide = batch > 1 and handle.ternel_tq1_linear_kernel(batch, N, K, 0) == 3  # TERNEL_TQ1_GEMM_WIDE
         names = WIDE_PHASES if wide else PHASES
         lay = PackedTensorLayout.for_tensor(N, K)
+        ring = ring_copies(packed_bytes(K, N))
         weights = [pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
                    for r in range(ring)]
         x = synthetic.device_activations(batch, K, seed=synthetic.SEED_BASE + 1 + i)
@@ -554,7 +566,7 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
         graph_ms = time_graph(graph_of(lambda: [gemv(weights[r % ring]) for r in range(ring * 4)])) / (ring * 4)
         phase_times = {phase: [] for phase in names if phase != "-"}
         spans, durations, by_start = [], {}, [[] for _ in range(4)]
-        for r in range(3):  # three cold launches, each over a copy last read 13 launches ago
+        for r in range(3):  # three cold launches, each over a copy not read for ring - 1 launches
             fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)
             gemv(weights[(r + 5) % ring])
             waves = fn(buf, max_waves, torch.cuda.current_stream(dev).cuda_stream)

@@ -208,6 +208,17 @@ _RETIRED: list[torch.Tensor] = []
 _CAPTURED: set[tuple[int, int]] = set()
 
 
+def _aligned_rows(x: torch.Tensor) -> torch.Tensor:
+    """``x`` contiguous and 16-byte aligned (the MFMA forms stage activations
+    with 16-byte loads): a view at an unaligned storage offset is copied."""
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone(memory_format=torch.contiguous_format)
+        if x.data_ptr() % 16:  # the caching allocator's blocks are 512-byte aligned
+            raise RuntimeError("could not obtain 16-byte aligned activations")
+    return x
+
+
 def _workspace_key(device: torch.device) -> tuple[int, int]:
     index = device.index if device.index is not None else torch.cuda.current_device()
     return index, torch.cuda.current_stream(torch.device("cuda", index)).cuda_stream
@@ -320,7 +331,7 @@ def tq1_gemm_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTenso
     if form_name == "direct" and batch > DIRECT_MAX_BATCH:
         raise FormatError(f"the direct-fragment form takes at most {DIRECT_MAX_BATCH} activation rows, got {batch}")
     form = GEMM_FORMS[form_name]
-    x = x.contiguous()
+    x = _aligned_rows(x)
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     need = handle.ternel_tq1_gemm_workspace_bytes(batch, layout.rows, layout.columns, form, config.k_split)
@@ -336,7 +347,7 @@ def tq1_linear_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTen
     """The library's own dispatch (``ternel_tq1_linear``) for a 2-D ``x``."""
     check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
-    x = x.contiguous()
+    x = _aligned_rows(x)
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     code = _DTYPE_CODE[x.dtype]
@@ -358,7 +369,7 @@ def tq1_swiglu_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTen
     if layout.rows % 2:
         raise FormatError(f"a SwiGLU weight interleaves gate and up rows, so its rows must be even, "
                           f"got {layout.rows}")
-    x = x.contiguous()
+    x = _aligned_rows(x)
     out = torch.empty((batch, layout.rows // 2), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     code = _DTYPE_CODE[x.dtype]
@@ -488,9 +499,30 @@ def tiled_from_words(packed: torch.Tensor, *, layout: PackedTensorLayout) -> tup
 
 # Packed words of (codes, scales) pairs the functional calls have seen, keyed by
 # the pair's identity and checked against their storage and version counters
-# on every hit; least recently used first, at most this many.
+# on every hit. An entry goes as soon as either tensor of its pair dies (a
+# weakref callback), so a pair's words never outlive it; beyond that the
+# cache keeps at most WORD_CACHE_ENTRIES entries and WORD_CACHE_BYTES of words,
+# least recently used first out.
 WORD_CACHE_ENTRIES = 1024
+WORD_CACHE_BYTES = 8 << 30
 _WORD_CACHE: OrderedDict[tuple[int, int], tuple] = OrderedDict()
+_word_cache_bytes = 0
+
+
+def _drop_word_entry(key: tuple[int, int], ref: weakref.ref | None = None) -> None:
+    """Remove one cache entry (only the one that registered ``ref`` when given:
+    a later entry may reuse the key once the first pair's ids are free)."""
+    global _word_cache_bytes
+    entry = _WORD_CACHE.get(key)
+    if entry is None or (ref is not None and entry[0] is not ref and entry[1] is not ref):
+        return
+    del _WORD_CACHE[key]
+    _word_cache_bytes -= entry[3].numel() * entry[3].element_size()
+
+
+def word_cache_bytes() -> int:
+    """Device bytes the functional calls' word cache holds now."""
+    return _word_cache_bytes
 
 
 def words_of(codes: torch.Tensor, scales: torch.Tensor, *, groups_per_row: int, tile: int) -> tuple[
@@ -498,6 +530,7 @@ def words_of(codes: torch.Tensor, scales: torch.Tensor, *, groups_per_row: int, 
     """Packed words (and layout) for the tiled pair, converted once and cached
     while both tensors live unchanged -- an in-place write bumps a tensor's
     version and forces a new conversion."""
+    global _word_cache_bytes
     layout = _tiled_layout(codes, scales, groups_per_row=groups_per_row, tile=tile)
     key = (id(codes), id(scales))
     stamp = (codes.data_ptr(), codes._version, scales.data_ptr(), scales._version, layout)
@@ -507,11 +540,19 @@ def words_of(codes: torch.Tensor, scales: torch.Tensor, *, groups_per_row: int, 
         if ref_codes() is codes and ref_scales() is scales and hit_stamp == stamp:
             _WORD_CACHE.move_to_end(key)
             return packed, layout
+        _drop_word_entry(key)
     packed = words_from_tiled(codes, scales, layout=layout)
-    _WORD_CACHE[key] = (weakref.ref(codes), weakref.ref(scales), stamp, packed)
-    _WORD_CACHE.move_to_end(key)
-    while len(_WORD_CACHE) > WORD_CACHE_ENTRIES:
-        _WORD_CACHE.popitem(last=False)
+    size = packed.numel() * packed.element_size()
+    if size > WORD_CACHE_BYTES:
+        return packed, layout
+    # The callbacks hold only the key and their own weakref: a dead tensor
+    # drops its entry without keeping the other one alive.
+    ref_codes = weakref.ref(codes, lambda r, key=key: _drop_word_entry(key, r))
+    ref_scales = weakref.ref(scales, lambda r, key=key: _drop_word_entry(key, r))
+    _WORD_CACHE[key] = (ref_codes, ref_scales, stamp, packed)
+    _word_cache_bytes += size
+    while len(_WORD_CACHE) > WORD_CACHE_ENTRIES or _word_cache_bytes > WORD_CACHE_BYTES:
+        _drop_word_entry(next(iter(_WORD_CACHE)))
     return packed, layout
 
 

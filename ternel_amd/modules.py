@@ -22,6 +22,8 @@ every ``nn.Embedding`` of a model for the packed twins.
 
 from __future__ import annotations
 
+import weakref
+
 import numpy as np
 import torch
 from torch import nn
@@ -106,8 +108,6 @@ class _PackedWeight(nn.Module):
         # The words are derived state: the state dict holds codes and scales.
         self.register_buffer("packed", torch.zeros(packed_shape(layout), dtype=torch.int32, device=device),
                              persistent=False)
-        self._tiled_key = None
-        self._tiled = None
 
     # -- loading --------------------------------------------------------------
     def load_blocks(self, blocks, *, validate: bool = True) -> None:
@@ -171,11 +171,11 @@ class _PackedWeight(nn.Module):
 
     # -- the reference's state ------------------------------------------------
     def _tiled_pair(self) -> tuple[torch.Tensor, torch.Tensor]:
-        key = (self.packed.data_ptr(), self.packed._version)
-        if self._tiled_key != key:
-            self._tiled = tiled_from_words(self.packed, layout=self.layout)
-            self._tiled_key = key
-        return self._tiled
+        # Derived on every access and not kept: the module holds one copy of
+        # the weight (the words), as the reference holds one (its codes and
+        # scales, src/ternel_mlx/modules.py:472-473,516-517). The state dict
+        # takes both arrays from one conversion.
+        return tiled_from_words(self.packed, layout=self.layout)
 
     @property
     def blocks(self) -> torch.Tensor:
@@ -335,10 +335,14 @@ class PackedEmbedding(_PackedWeight):
         derived from the packed words on first use and again whenever they are
         replaced or written. Not part of the state dict. Call it once before
         capturing a graph that gathers, so the capture holds no rebuild."""
-        key = (self.packed.data_ptr(), self.packed._version, self.packed.device)
-        if getattr(self, "_row_blocks_key", None) != key:
+        # Keyed on the words tensor itself (a weak reference, so a replaced
+        # tensor whose storage the allocator hands to the next load can never
+        # match) and its version counter (in-place writes).
+        source = getattr(self, "_row_blocks_source", None)
+        if source is None or source() is not self.packed or self._row_blocks_version != self.packed._version:
             self._row_blocks = unpack_weights(self.packed, layout=self.layout)
-            self._row_blocks_key = key
+            self._row_blocks_source = weakref.ref(self.packed)
+            self._row_blocks_version = self.packed._version
         return self._row_blocks
 
     def as_linear(self, x: torch.Tensor) -> torch.Tensor:

@@ -233,8 +233,9 @@ def test_split_k_refusal_message() -> None:
 def test_workspace_queries() -> None:
     handle = _lib.lib()
     # every split workspace: a fixed 64 KiB counter region (its last word the
-    # error word), then fp32 partials
-    counters = 64 * 1024
+    # error word), the row GEMV's region of counters and piece slots (2 KiB +
+    # two 512-byte slots for each of 512 workgroups), then fp32 partials
+    counters = 64 * 1024 + 2048 + 2 * 512 * 512
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 17408, 5120, 0, 0) == counters + 10 * 17408 * 4
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 17408, 0, 0) == counters + 17 * 5120 * 4
     assert handle.ternel_tq1_swiglu_workspace_bytes(1, 34816, 5120, 0) == counters + 10 * 34816 * 4
