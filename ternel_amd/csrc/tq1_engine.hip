@@ -33,6 +33,7 @@
 #include <atomic>
 #include <mutex>
 #include <set>
+#include <string>
 #include <utility>
 #include <type_traits>
 
@@ -921,530 +922,259 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// row_gemv_kernel: the M = 1 decode GEMV (one activation vector), laid out so
-// that a 64-row tile's K reduction stays inside one CU wherever the shape
-// allows, and every wave streams its own weight words from its first
-// instructions (the LUT23 algorithm of src/ternel_mlx/kernels.py:244-342).
+// strip_gemv_kernel: the M = 1 decode GEMV (one activation vector) for
+// matrices of at most kStripMaxGroups groups per row (K <= 5120) and at most
+// 62 rows per CU, with every row's K reduction inside one workgroup (the
+// LUT23 algorithm of src/ternel_mlx/kernels.py:244-342).
 //
-// Work is (tile, group) items. With T 64-row tiles and P workgroups (one per
-// CU), workgroup b owns the F = T / P whole tiles [b F, (b+1) F); the
-// R = T - P F remaining tiles' R G items are dealt out in contiguous runs,
-// workgroup b taking [b R G / P, (b+1) R G / P). A workgroup lists its
-// remainder items first, then its whole tiles, and its 16 waves take
-// contiguous runs of that list. Each wave builds the LUT23 tables of its own
-// items (they depend only on the group's 128 activations) in its own LDS
-// buffer and sums its own rows, one lane per row, so no wave waits for
-// another until a tile's partial sums are combined:
-//  - inside the workgroup through LDS: the waves sharing a tile store their
-//    partials and count in on an LDS counter; the last to arrive adds them in
-//    wave order;
-//  - across workgroups (remainder tiles only) through 64-bit slots in the
-//    workspace holding {partial, tag 1}: the workgroup's combining wave
-//    stores its slot and counts in on the tile's counter; the last of the
-//    tile's k contributors waits (bounded) until every slot carries its tag,
-//    adds them in workgroup order, writes y, and returns counter and slots to
-//    zero. A partial travels in the same atomic word as the tag that marks
-//    it, so nothing else needs ordering; the counter only elects the reducer,
-//    who waits only for contributors that have already counted in (their
-//    slot stores precede their count). Remainder items come first in every
-//    list, so where workgroups also own whole tiles (the 17408-row gate/up:
-//    one tile each plus 2.5 groups of the 16 leftover tiles) those tiles are
-//    finished early in the launch.
-// Summation order: per wave, groups in K order into one fp32 accumulator
-// (acc = fma(scale, sum, acc), each block's sum in the reference's slot
-// order), then a tile's wave partials in wave order and its workgroup
-// partials in workgroup order -- fixed for a shape, so a result is
-// bit-identical from run to run, and when one wave holds a whole row (one
-// group per row) it is the reference's order exactly.
-// A reducer that gives up, or that finds the workspace error word already set
-// by an earlier give-up, writes NaN rows and sets the error word (value 4):
-// such a workspace refuses until it is zeroed again.
+// One workgroup per CU owns a strip of R < 64 rows: strip s holds rows
+// [2 floor(s U / P), 2 floor((s + 1) U / P)), U = ceil(N / 2), so strips
+// differ by at most two rows and a gate/up pair never straddles two of them.
+// Workgroup b takes strip (b % 8) P / 8 + b / 8 when P is a multiple of 8:
+// workgroups are dealt to the eight XCDs in turn, so each XCD holds adjacent
+// strips and a cache line shared by two strips is read into one L2.
+// The workgroup stages the activations in LDS (one 16-byte load per thread,
+// waited for before any weight word is requested: behind the chip-wide
+// burst of word loads they came back ~2 us later) and builds the LUT23
+// tables of all G groups once (G x 927 floats, 148,320 bytes at G = 40);
+// they stay for the whole launch, so a lane may look up any group. The
+// strip's R x G blocks are numbered t = g R + i (row i, group g), so
+// consecutive lanes read consecutive rows of one group, and cut into items
+// of 64; the 16 waves take contiguous runs of items, each keeping the next
+// item's words in flight while it sums one. Every load is issued
+// unconditionally (past the end of a run a wave re-reads the item it sums,
+// from cache), so the compiler's wait counts stay exact: a wait for one item
+// never waits for the next.
+// Sums: a block's in the reference's slot order; its scale * sum stored
+// alone; a row adds its G values in group order. The order is fixed by the
+// shape, so results are bit-identical from run to run, and equal the
+// reference's to within fp32 reassociation of the per-group terms.
+// No workspace, no memory shared between workgroups.
+// (Strips of 64 rows or more run the (tile, group) LUT23 kernel above:
+// rebuilding all G tables per CU there costs more than its fix-up.)
 // ---------------------------------------------------------------------------
-constexpr int kRowWaves = 16;
-constexpr int kRowThreads = kRowWaves * 64;
-// One item's tables, padded so that every table task writes whole 16-byte
-// runs: L3 slot s at [28 s, 28 s + 27), the tail at [700, 727), L2 slot s at
-// [728 + 12 s, 728 + 12 s + 9). A code byte's high digit reaches 28 at most
-// (illegal bytes), which stays inside the next slot's table or the tail.
-constexpr int kRowL3Stride = 28;
-constexpr int kRowTailBase = kFullSlots * kRowL3Stride;         // 700
-constexpr int kRowL2Base = kRowTailBase + kRowL3Stride;          // 728
-constexpr int kRowL2Stride = 12;
-constexpr int kRowTableFloats = kRowL2Base + kFullSlots * kRowL2Stride;  // 1028
-constexpr int kRowTableBuffers = 2;
-// Workspace region of the cross-workgroup slots: counters for at most
-// kRowMaxWorkgroups remainder tiles, then two 64-row slots per workgroup.
-constexpr int kRowMaxWorkgroups = 512;
-constexpr int kRowCounterBytes = kRowMaxWorkgroups * 4;
-constexpr int kRowSlotBytes = kTileRows * 8;
-constexpr size_t kRowRegionBytes = kRowCounterBytes + size_t{2} * kRowMaxWorkgroups * kRowSlotBytes;
-constexpr unsigned kRowGiveUpBit = 4u;
+constexpr int kStripWaves = 16;
+constexpr int kStripThreads = kStripWaves * 64;
+constexpr int kStripMaxGroups = 40;
+constexpr int kStripMaxRows = 62;
+constexpr int kStripLdsFloats = 40960;  // 160 KiB, the workgroup limit
+static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows <= kStripLdsFloats, "LDS fits");
+constexpr int kStripTrit3Iters = (kStripMaxGroups * (kFullSlots + 1) + kStripThreads - 1) / kStripThreads;
+constexpr int kStripL2Iters = (kStripMaxGroups * kFullSlots + kStripThreads - 1) / kStripThreads;
+// Below this many rows the LUT23 kernel is used instead (equal speed).
+constexpr int kStripMinRows = 2048;
 
-struct RowGeometry {
+struct StripGeometry {
     int N, G;
-    int full;       // F: whole tiles per workgroup
-    int rem_tiles;  // R
-    int P;          // workgroups
-    int Pr;         // workgroups holding leftover items: min(P, R G), each at least one
-    int spin_limit;
+    int P;
+    int units;       // U = ceil(N / 2)
+    int value_base;  // LDS float offset of the block values (and, before them, the staged activations)
 };
 
-// First leftover item of workgroup b (the run of b is [begin(b), begin(b + 1))).
-// The host keeps Pr * R * G below 2^31, so 32-bit arithmetic is exact.
-__device__ __forceinline__ int row_rem_begin(int b, const RowGeometry &geo) {
-    const int RG = geo.rem_tiles * geo.G;
-    return b >= geo.Pr ? RG : static_cast<int>(static_cast<unsigned>(b * RG) / static_cast<unsigned>(geo.Pr));
+// First row of strip s.
+__device__ __forceinline__ int strip_row(int s, const StripGeometry &geo) {
+    return min(geo.N, 2 * static_cast<int>(static_cast<unsigned>(s * geo.units) / static_cast<unsigned>(geo.P)));
 }
 
-// The workgroups [lo, hi] holding items of leftover tile q, and the slot the
-// first of them uses for it (1 when q is not that workgroup's first tile).
-struct RowSplit {
-    int lo, hi, lo_slot;
-};
-
-__device__ __forceinline__ RowSplit row_split(int q, const RowGeometry &geo) {
-    const unsigned RG = static_cast<unsigned>(geo.rem_tiles * geo.G);
-    const unsigned q0 = static_cast<unsigned>(q * geo.G);
-    RowSplit sp;
-    sp.lo = static_cast<int>(((q0 + 1) * geo.Pr + RG - 1) / RG) - 1;
-    sp.hi = static_cast<int>(((q0 + geo.G) * geo.Pr + RG - 1) / RG) - 1;
-    sp.lo_slot = row_rem_begin(sp.lo, geo) == static_cast<int>(q0) ? 0 : 1;
-    return sp;
-}
-
-// The activations of one item's table tasks: lanes 0-24 the L3 table of slot
-// l (x[5l + 2 .. 5l + 4]), lane 25 the tail (x[125 .. 127]), lanes 26-50 the
-// L2 table of slot l - 26 (x[5s], x[5s + 1]; a third value is read and not
-// used), lanes 51-63 nothing (they read x[0 .. 2]).
-__device__ __forceinline__ int row_task_position(int lane) {
-    return lane < kFullSlots ? 5 * lane + 2 : (lane == kFullSlots ? 125 : (lane <= 2 * kFullSlots ? 5 * (lane - 26) : 0));
-}
-
+// The table tasks of one thread: three-trit task t < 26 G is (group t / 26,
+// slot t % 26; slot 25 the tail), two-trit task t < 25 G is (group t / 25,
+// slot t % 25). gather() reads their activations (from LDS or global memory,
+// every read issued, indices clamped), build() writes the tables from them,
+// as build_lut_tables computes them.
 template <typename T>
-struct RowTaskX {
-    T u, v, w;
-};
+struct StripTasks {
+    T v3[kStripTrit3Iters][3], v2[kStripL2Iters][2];
 
-// The tables of one item from its task activations, written as single
-// dwords (no register packing). Finite values take the short form: the nine
-// two-trit sums P[i + 3 j] = (i - 1) u + (j - 1) v are -(u+v), -v, u-v, -u,
-// 0, u, -(u-v), v, u+v (the reference's a + b for every finite pair up to the
-// sign of a zero sum), and the three-trit entries are P - w, P, P + w, the
-// reference's (a + b) + d. Non-finite activations take the literal products
-// (t - 1) * x, so 0 * inf gives NaN as in the reference.
-// Writes one table task's entries: P (and, for a three-trit table, P - w
-// before it and P + w after it, q0 / q2) through a store address laundered by
-// an empty asm, so the compiler cannot prove 16-byte alignment and pairs the
-// stores as ds_write2_b32 from wherever the values sit (for ds_write_b128 it
-// moved them into aligned register quads first: 19 moves per item).
-__device__ __forceinline__ void row_write_tables(float *table, int lane, const float (&q0)[9], const float (&p)[9],
-                                                 const float (&q2)[9]) {
-    typedef __attribute__((address_space(3))) float lds_float;
-    uint32_t where = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_float *)(table))) +
-                     4u * static_cast<uint32_t>(lane <= kFullSlots ? lane * kRowL3Stride
-                                                                   : kRowL2Base + (lane - 26) * kRowL2Stride);
-    asm volatile("" : "+v"(where));
-    lds_float *const dst = (lds_float *)(static_cast<uintptr_t>(where));
-    if (lane <= kFullSlots) {
+    __device__ __forceinline__ void gather(const T *xs, int G, int tid) {
 #pragma unroll
-        for (int e = 0; e < 9; ++e) {
-            dst[e] = q0[e];
-            dst[9 + e] = p[e];
-            dst[18 + e] = q2[e];
-        }
-    } else if (lane <= 2 * kFullSlots) {
-#pragma unroll
-        for (int e = 0; e < 9; ++e) dst[e] = p[e];
-    }
-}
-
-// The tables of one item from its task activations. Finite values take the
-// short form: the nine two-trit sums P[i + 3 j] = (i - 1) u + (j - 1) v are
-// -(u+v), -v, u-v, -u, 0, u, -(u-v), v, u+v (the reference's a + b for every
-// finite pair up to the sign of a zero sum), and the three-trit entries are
-// P - w, P, P + w, the reference's (a + b) + d. Non-finite activations take
-// the literal products (t - 1) * x, so 0 * inf gives NaN as in the reference.
-// Each form writes its own entries (no register merge of the two).
-template <typename T>
-__device__ __forceinline__ void row_build_tables(float *table, const RowTaskX<T> &tx, int lane) {
-    const float u = to_f32<T>(tx.u), v = to_f32<T>(tx.v), w = to_f32<T>(tx.w);
-    const bool bad = !__builtin_isfinite(u) || !__builtin_isfinite(v) || !__builtin_isfinite(w);
-    float p[9], q0[9], q2[9];
-    if (__builtin_expect(__any(bad), 0)) {
-        const float mu[3] = {-1.0f * u, 0.0f * u, 1.0f * u};
-        const float mv[3] = {-1.0f * v, 0.0f * v, 1.0f * v};
-        float q1[9];
-#pragma unroll
-        for (int e = 0; e < 9; ++e) {
-            p[e] = mu[e % 3] + mv[e / 3];
-            q0[e] = p[e] + -1.0f * w;
-            q1[e] = p[e] + 0.0f * w;
-            q2[e] = p[e] + 1.0f * w;
-        }
-        // L2 lanes write P, three-trit lanes P + 0 * w in the middle third.
-        if (lane <= kFullSlots) {
-#pragma unroll
-            for (int e = 0; e < 9; ++e) p[e] = q1[e];
-        }
-        row_write_tables(table, lane, q0, p, q2);
-        return;
-    }
-    const float s = u + v, d = u - v;
-    p[0] = -s;
-    p[1] = -v;
-    p[2] = d;
-    p[3] = -u;
-    p[4] = 0.0f;
-    p[5] = u;
-    p[6] = -d;
-    p[7] = v;
-    p[8] = s;
-#pragma unroll
-    for (int e = 0; e < 9; ++e) {
-        q0[e] = p[e] - w;
-        q2[e] = p[e] + w;
-    }
-    row_write_tables(table, lane, q0, p, q2);
-}
-
-// One block of one row: its 25 code bytes' table pairs and the tail entry,
-// read from the item's tables at byte address `base` (all reads issued
-// before any is used).
-struct RowLookups {
-    float l2[kFullSlots], l3[kFullSlots], tail;
-};
-
-__device__ __forceinline__ void row_lookups(RowLookups &r, const uint32_t (&w)[kBlockWords], const char *lds,
-                                            uint32_t base) {
-    auto l2 = [&](uint32_t address, int s) {
-        return *reinterpret_cast<const float *>(lds + address + (kRowL2Base + s * kRowL2Stride) * 4);
-    };
-    auto l3 = [&](uint32_t address, int s) {
-        return *reinterpret_cast<const float *>(lds + address + s * kRowL3Stride * 4);
-    };
-    {
-        // Word 0: scale bytes, then code bytes 0 and 1 (bytes 2 and 3 moved
-        // to the 16-bit halves by one byte permute).
-        uint32_t lo_a, hi_a, lo_b, hi_b;
-        split_pair(__builtin_amdgcn_perm(0u, w[0], 0x0c030c02u), base, lo_a, hi_a, lo_b, hi_b);
-        r.l2[0] = l2(lo_a, 0);
-        r.l3[0] = l3(hi_a, 0);
-        r.l2[1] = l2(lo_b, 1);
-        r.l3[1] = l3(hi_b, 1);
-    }
-#pragma unroll
-    for (int word = 1; word < kBlockWords; ++word) {
-        uint32_t lo[4], hi[4];
-        split_word(w[word], base, lo, hi);
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int s = word * 4 + b - 2;
-            if (s >= kFullSlots) continue;
-            r.l2[s] = l2(lo[b], s);
-            r.l3[s] = l3(hi[b], s);
-        }
-    }
-    const uint32_t tail = base + 4 * tq1_bytes::tail_entry(w[6] >> 24);
-    r.tail = *reinterpret_cast<const float *>(lds + tail + kRowTailBase * 4);
-}
-
-// The block's sum in the reference's slot order: pair(0) + pair(1) + ... +
-// pair(24) + tail, pair(s) = L2 + L3.
-__device__ __forceinline__ float row_sum(const RowLookups &r) {
-    float sum = r.l2[0] + r.l3[0];
-#pragma unroll
-    for (int s = 1; s < kFullSlots; ++s) sum += r.l2[s] + r.l3[s];
-    return sum + r.tail;
-}
-
-// A finished tile's rows: y[row] (or, GLU, SiLU(gate) * up from the even
-// lane of each gate/up pair into the half-width output).
-template <typename T, bool GLU>
-__device__ __forceinline__ void row_store(T *__restrict__ y, int N, int tile, int lane, float v) {
-    const int row = tile * kTileRows + lane;
-    if constexpr (GLU) {
-        const T own = from_f32<T>(v);
-        const float partner = __shfl_xor(to_f32<T>(own), 1, 64);
-        if (row < N && (lane & 1) == 0) y[row / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
-    } else {
-        if (row < N) y[row] = from_f32<T>(v);
-    }
-}
-
-// Leftover tile q's reduction across its workgroups [sp_lo, sp_hi], by the
-// one whose count made the total a multiple of k (`old` is lane 0's answer):
-// every other slot added in workgroup order once its tag is there (a batch of
-// loads in flight at once), the rows written, counter and slots returned to
-// zero. A reducer that gives up, or finds the error word set by an earlier
-// give-up, writes NaN rows and sets the word.
-template <typename T, bool GLU>
-__device__ __forceinline__ void row_reduce(T *__restrict__ y, const RowGeometry geo, unsigned *__restrict__ legacy,
-                                           unsigned *__restrict__ row_counters,
-                                           unsigned long long *__restrict__ slots, int b, int q, int tile, int sp_lo,
-                                           int sp_hi, int sp_lo_slot, float value, unsigned old) {
-    const int lane = threadIdx.x & 63;
-    const int k = sp_hi - sp_lo + 1;
-    old = __shfl(old, 0, 64);
-    if ((old + 1) % static_cast<unsigned>(k) != 0) return;
-    TQ1_PHASE(b * kRowWaves + (threadIdx.x >> 6), 5);  // reducer starts
-    unsigned long long *lane_slots = slots + lane;
-    auto slot = [&](int c) { return lane_slots + (c * 2 + (c == sp_lo ? sp_lo_slot : 0)) * kTileRows; };
-    bool ok = geo.spin_limit >= 0 &&
-              __hip_atomic_load(legacy + kWorkspaceErrorSlot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u;
-    float total = 0.0f;
-    constexpr int kBatch = 16;
-    for (int c0 = sp_lo; c0 <= sp_hi; c0 += kBatch) {
-        unsigned long long v[kBatch];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int c = min(c0 + u, sp_hi);
-            v[u] = c == b ? ((1ull << 32) | __float_as_uint(value))
-                          : __hip_atomic_load(slot(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int it = 0; it < kStripTrit3Iters; ++it) {
+            const int t = min(tid + it * kStripThreads, G * (kFullSlots + 1) - 1);
+            const int g = t / (kFullSlots + 1), s = t - g * (kFullSlots + 1);
+            const T *p = xs + g * kBlockWeights + (s < kFullSlots ? 5 * s + 2 : 125);
+            v3[it][0] = p[0];
+            v3[it][1] = p[1];
+            v3[it][2] = p[2];
         }
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int c = c0 + u;
-            if (c <= sp_hi) {
-                for (int spin = 0; (v[u] >> 32) != 1ull && ok; ++spin) {
-                    if (spin >= geo.spin_limit) ok = false;
-                    __builtin_amdgcn_s_sleep(1);
-                    v[u] = __hip_atomic_load(slot(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                const float part = __uint_as_float(static_cast<uint32_t>(v[u]));
-                total = c == sp_lo ? part : total + part;
+        for (int it = 0; it < kStripL2Iters; ++it) {
+            const int t = min(tid + it * kStripThreads, G * kFullSlots - 1);
+            const int g = t / kFullSlots, s = t - g * kFullSlots;
+            const T *p = xs + g * kBlockWeights + 5 * s;
+            v2[it][0] = p[0];
+            v2[it][1] = p[1];
+        }
+    }
+
+    __device__ __forceinline__ void build(float *lut, int G, int tid) const {
+#pragma unroll
+        for (int it = 0; it < kStripTrit3Iters; ++it) {
+            const int t = tid + it * kStripThreads;
+            if (t < G * (kFullSlots + 1)) {
+                const int g = t / (kFullSlots + 1), s = t - g * (kFullSlots + 1);
+                const float x0 = to_f32<T>(v3[it][0]), x1 = to_f32<T>(v3[it][1]), x2 = to_f32<T>(v3[it][2]);
+                const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
+                const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
+                const float d[3] = {-1.0f * x2, 0.0f * x2, 1.0f * x2};
+                float pair[kL2Entries];
+#pragma unroll
+                for (int e = 0; e < kL2Entries; ++e) pair[e] = a[e % 3] + b[e / 3];
+                float *dst = lut + g * kLutFloats + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
+#pragma unroll
+                for (int e = 0; e < kL3Entries; ++e) dst[e] = pair[e % 9] + d[e / 9];
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kStripL2Iters; ++it) {
+            const int t = tid + it * kStripThreads;
+            if (t < G * kFullSlots) {
+                const int g = t / kFullSlots, s = t - g * kFullSlots;
+                const float x0 = to_f32<T>(v2[it][0]), x1 = to_f32<T>(v2[it][1]);
+                const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
+                const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
+                float *dst = lut + g * kLutFloats + s * kL2Entries;
+#pragma unroll
+                for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
             }
         }
     }
-    TQ1_PHASE(b * kRowWaves + (threadIdx.x >> 6), 6);  // every slot read
-    // Every lane of the wave must agree (a lane's wait may end early).
-    if (!__all(ok)) {
-        if (lane == 0)
-            __hip_atomic_fetch_or(legacy + kWorkspaceErrorSlot, kRowGiveUpBit, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-        row_store<T, GLU>(y, geo.N, tile, lane, __builtin_nanf(""));
-        return;
+};
+
+// One block's LUT23 sum from its words and its group's tables at byte
+// offset `table`: slot 0..24 in order, then the tail (the reference's order).
+__device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords], const char *lds, uint32_t table) {
+    auto at = [&](uint32_t address, int entry) {
+        return *reinterpret_cast<const float *>(lds + address + entry * 4);
+    };
+    float sum = 0.0f;
+#pragma unroll
+    for (int word = 0; word < kBlockWords; ++word) {
+        uint32_t lo[4], hi[4];
+        split_word(w[word], table, lo, hi);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
+            if (s < 0 || s >= kFullSlots) continue;
+            const float pair = at(lo[b], s * kL2Entries) + at(hi[b], kL3Base + s * kL3Entries);
+            sum = s == 0 ? pair : sum + pair;
+        }
     }
-    row_store<T, GLU>(y, geo.N, tile, lane, total);
-    for (int c = sp_lo; c <= sp_hi; ++c) __hip_atomic_store(slot(c), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (lane == 0) __hip_atomic_store(row_counters + q, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return sum + at(table + 4 * tq1_bytes::tail_entry(w[6] >> 24), kTailBase);
 }
 
 template <typename T, bool GLU>
-__global__ __launch_bounds__(kRowThreads, 1) void row_gemv_kernel(const uint32_t *__restrict__ packed,
-                                                                  const T *__restrict__ x, T *__restrict__ y,
-                                                                  unsigned *__restrict__ legacy_counters,
-                                                                  unsigned *__restrict__ row_counters,
-                                                                  unsigned long long *__restrict__ row_slots,
-                                                                  RowGeometry geo) {
-    __shared__ __align__(16) float tables[kRowWaves][kRowTableBuffers][kRowTableFloats];
-    __shared__ float partials[kRowWaves][2][kTileRows];
-    __shared__ unsigned arrivals[kRowWaves];
-    __shared__ int wave_first_tile[kRowWaves];
+__device__ __forceinline__ void strip_store(T *__restrict__ y, int row, int lane, bool valid, float v) {
+    if constexpr (GLU) {
+        const T own = from_f32<T>(v);
+        const float partner = __shfl_xor(to_f32<T>(own), 1, 64);
+        if (valid && (lane & 1) == 0) y[row / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
+    } else {
+        if (valid) y[row] = from_f32<T>(v);
+    }
+}
+
+// STAGE: the activations are a 2-byte type at a 16-byte aligned address and
+// are staged in LDS with one 16-byte load per thread; otherwise each thread
+// reads its table tasks' activations from global memory.
+template <typename T, bool GLU, bool STAGE>
+__global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint32_t *__restrict__ packed,
+                                                                      const T *__restrict__ x, T *__restrict__ y,
+                                                                      StripGeometry geo) {
+    __shared__ __align__(16) float lds_f[kStripLdsFloats];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.x;
     const int G = geo.G;
-    const int row_wave_id = b * kRowWaves + wave;
-    (void)row_wave_id;
-    TQ1_PHASE(row_wave_id, 0);
-    TQ1_PHASE_XCC(row_wave_id);
+    const int strip_wave_id = b * kStripWaves + wave;
+    (void)strip_wave_id;
+    TQ1_PHASE(strip_wave_id, 0);
+    TQ1_PHASE_XCC(strip_wave_id);
 
-    // This workgroup's list: n_rem leftover items from leftover item
-    // rem_begin, then F whole tiles from tile b F. Wave v takes the items
-    // [v n / 16, (v + 1) n / 16). Items are numbered globally tile * G +
-    // group, so a wave's items are at most two contiguous runs: A (leftover
-    // items) and B (whole-tile items).
-    const int rem_begin = row_rem_begin(b, geo);
-    const int n_rem = row_rem_begin(b + 1, geo) - rem_begin;
-    const int n = n_rem + geo.full * G;
-    const int rem_tile0 = geo.P * geo.full;
-    const int i0 = (wave * n) >> 4;
-    const int i1 = ((wave + 1) * n) >> 4;
-    const int cnt = i1 - i0;
-    const int len_a = max(0, min(i1, n_rem) - i0);
-    const int a0 = rem_tile0 * G + rem_begin + i0;                  // first global item of run A
-    const int b0 = b * geo.full * G + max(i0, n_rem) - n_rem;       // first global item of run B
-    const int first_item = len_a > 0 ? a0 : b0;
-    const int first_tile = cnt > 0 ? first_item / G : -1;
+    // Activations first.
+    constexpr int kVec = 16 / static_cast<int>(sizeof(T));
+    static_assert(!STAGE || sizeof(T) == 2, "staging takes 2-byte activations");
+    const int pieces = G * (kBlockWeights / kVec);
+    StripTasks<T> tasks;
+    uint4 piece;
+    if constexpr (STAGE)
+        piece = reinterpret_cast<const uint4 *>(x)[min(tid, pieces - 1)];
+    else
+        tasks.gather(x, G, tid);
 
-    // Load cursor (global item, group), shared by the words and the task
-    // activations of the item loaded next.
-    int lk = 0, lgi = first_item, lg = first_item - first_tile * G;
-    const uint32_t *const lane_words = packed + lane;
-    const T *const lane_x = x + row_task_position(lane);
-    auto load_item = [&](uint32_t (&wd)[kBlockWords], RowTaskX<T> &tx) __attribute__((always_inline)) {
-        // Task activations first: a wait for them never waits for these words.
-        const T *px = lane_x + lg * kBlockWeights;
-        tx.u = px[0];
-        tx.v = px[1];
-        tx.w = px[2];
-        const uint32_t *pw = lane_words + static_cast<int64_t>(lgi) * kTileGroupWords;
+    const int s = (geo.P & 7) == 0 ? (b & 7) * (geo.P >> 3) + (b >> 3) : b;
+    const int lo = strip_row(s, geo);
+    const int R = strip_row(s + 1, geo) - lo;
+    const int RG = R * G;
+    const int n_items = (RG + 63) >> 6;
+    const int i0 = (wave * n_items) >> 4;
+    const int i1 = ((wave + 1) * n_items) >> 4;
+    const float inv_r = 1.0f / static_cast<float>(max(R, 1));
+
+    // Block t = g R + i of item i for this lane (clamped into the strip):
+    // its group and its word offset.
+    auto block = [&](int item, int &t, int &g) __attribute__((always_inline)) {
+        t = (item << 6) + lane;
+        const int tc = min(t, max(RG - 1, 0));
+        g = static_cast<int>((static_cast<float>(tc) + 0.5f) * inv_r);
+        const int row = lo + (tc - g * R);
+        return ((row >> 6) * G + g) * kTileGroupWords + (row & 63);
+    };
+    // (The scheduling barriers keep the sums of the item before from moving
+    // above the loads, where they would wait for that item's words first.)
+    auto load = [&](int item, uint32_t (&w)[kBlockWords]) __attribute__((always_inline)) {
+        int t, g;
+        const uint32_t *p = packed + block(item, t, g);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < kBlockWords; ++j) wd[j] = pw[j * kTileRows];
-        ++lk;
-        ++lgi;
-        if (++lg == G) lg = 0;
-        if (lk == len_a) {
-            lgi = b0;
-            lg = b0 % G;
-        }
+        for (int j = 0; j < kBlockWords; ++j) w[j] = p[j * kTileRows];
+        __builtin_amdgcn_sched_barrier(0);
     };
 
-    // The first two items' loads go out before anything else.
-    uint32_t w0[kBlockWords], w1[kBlockWords], w2[kBlockWords];
-    RowTaskX<T> x0, x1, x2;
-    if (cnt > 0) load_item(w0, x0);
-    if (cnt > 1) load_item(w1, x1);
-    TQ1_PHASE(row_wave_id, 1);  // first loads issued
+    wait_vector_memory();
+    uint32_t wa[kBlockWords], wb[kBlockWords];
+    load(min(i0, n_items - 1), wa);
+    TQ1_PHASE(strip_wave_id, 1);  // activations arrived, first words issued
 
-    if (lane == 0) wave_first_tile[wave] = first_tile;
-    if (tid < kRowWaves) arrivals[tid] = 0u;
-    // The leftover tiles this workgroup shares with others can only be its
-    // first (qa) and last (qz) ones: their contributors, found once.
-    const int qa = n_rem > 0 ? rem_begin / G : -1;
-    const int qz = n_rem > 0 ? (rem_begin + n_rem - 1) / G : -1;
-    int a_lo = 0, a_hi = 0, a_slot = 0, z_lo = 0, z_hi = 0, z_slot = 0;
-    if (n_rem > 0) {
-        const RowSplit sa = row_split(qa, geo), sz = row_split(qz, geo);
-        a_lo = sa.lo;
-        a_hi = sa.hi;
-        a_slot = sa.lo_slot;
-        z_lo = sz.lo;
-        z_hi = sz.hi;
-        z_slot = sz.lo_slot;
+    if constexpr (STAGE) {
+        T *const xs = reinterpret_cast<T *>(lds_f + geo.value_base);
+        if (tid < pieces) reinterpret_cast<uint4 *>(xs)[tid] = piece;
+        __syncthreads();
+        tasks.gather(xs, G, tid);
     }
+    tasks.build(lds_f, G, tid);
+    __syncthreads();
+    TQ1_PHASE(strip_wave_id, 2);  // tables ready
+
+    const char *const lds = reinterpret_cast<const char *>(lds_f);
+    auto consume = [&](int item, const uint32_t (&w)[kBlockWords]) __attribute__((always_inline)) {
+        int t, g;
+        (void)block(item, t, g);
+        const float sum = strip_block_sum(w, lds, static_cast<uint32_t>(g * kLutFloats * 4));
+        if (t < RG) lds_f[geo.value_base + t] = half_bits_to_float(w[0]) * sum;
+    };
+    // No branch separates a load from the loop's other loads, so every path
+    // into the loop head carries the same seven loads in flight.
+    for (int k = i0; k < i1; k += 2) {
+        load(min(k + 1, i1 - 1), wb);
+        consume(k, wa);
+        load(min(k + 2, i1 - 1), wa);
+        if (k + 1 < i1) consume(k + 1, wb);
+    }
+    TQ1_PHASE(strip_wave_id, 3);  // all items summed
     __syncthreads();
 
-    const char *const lds = reinterpret_cast<const char *>(&tables[0][0][0]);
-    const uint32_t table_base0 = static_cast<uint32_t>(wave * kRowTableBuffers * kRowTableFloats * 4);
-
-    // Shared leftover tiles are published (slot stored, count issued) as soon
-    // as the workgroup's partial exists; the count's answer is read, and the
-    // tile reduced by its last contributor, only after this wave's items, so
-    // no wave stalls on that round trip inside its loop. A wave publishes at
-    // most two such tiles: its first and its last.
-    int pend_n = 0, pend_q0 = 0, pend_q1 = 0;
-    float pend_v0 = 0.0f, pend_v1 = 0.0f;
-    unsigned pend_old0 = 0, pend_old1 = 0;
-
-    // Hands one finished tile partial on: combined inside the workgroup, then
-    // written (a whole tile, or a leftover tile this workgroup holds alone)
-    // or published for the reduction across workgroups.
-    auto contribute = [&](int tile, float value) __attribute__((always_inline)) {
-        // The workgroup's items of this tile: [a, e).
-        int a, e;
-        if (tile < rem_tile0) {
-            a = n_rem + (tile - b * geo.full) * G;
-            e = a + G;
-        } else {
-            const int q0 = (tile - rem_tile0) * G;
-            a = max(q0, rem_begin) - rem_begin;
-            e = min(q0 + G, rem_begin + n_rem) - rem_begin;
+    // Row i by lane i of wave 0: its G block values in group order.
+    if (wave == 0) {
+        float total = 0.0f;
+        if (lane < R) {
+            const float *v = lds_f + geo.value_base + lane;
+            total = v[0];
+            for (int g = 1; g < G; ++g) total += v[g * R];
         }
-        const int wf = (kRowWaves * a + kRowWaves - 1) / n;
-        const int wl = (kRowWaves * (e - 1) + kRowWaves - 1) / n;
-        if (wf != wl) {
-            partials[wave][first_tile == tile ? 0 : 1][lane] = value;
-            // Waves with no items in between do not count in.
-            unsigned expect = static_cast<unsigned>(wl - wf);
-            if (n < kRowWaves) {
-                expect = 0;
-                for (int v = wf + 1; v <= wl; ++v) expect += ((v + 1) * n) >> 4 > ((v * n) >> 4) ? 1u : 0u;
-            }
-            unsigned old = 0;
-            if (lane == 0)
-                old = __hip_atomic_fetch_add(&arrivals[wf], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-            old = __shfl(old, 0, 64);
-            if (old != expect) return;
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-            float total = 0.0f;
-            for (int v = wf; v <= wl; ++v) {
-                if (((v + 1) * n) >> 4 == (v * n) >> 4) continue;
-                const float part = partials[v][wave_first_tile[v] == tile ? 0 : 1][lane];
-                total = v == wf ? part : total + part;
-            }
-            value = total;
-        }
-        const int q = tile - rem_tile0;
-        const bool shared = q >= 0 && (q == qa ? a_lo != a_hi : (q == qz && z_lo != z_hi));
-        if (!shared) {
-            row_store<T, GLU>(y, geo.N, tile, lane, value);
-            return;
-        }
-        const int lo = q == qa ? a_lo : z_lo;
-        const int lo_slot = q == qa ? a_slot : z_slot;
-        unsigned long long *mine = row_slots + lane + (b * 2 + (b == lo ? lo_slot : 0)) * kTileRows;
-        __hip_atomic_store(mine, (1ull << 32) | __float_as_uint(value), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        unsigned old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(row_counters + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool second = pend_n != 0;
-        pend_q0 = second ? pend_q0 : q;
-        pend_v0 = second ? pend_v0 : value;
-        pend_old0 = second ? pend_old0 : old;
-        pend_q1 = second ? q : pend_q1;
-        pend_v1 = second ? value : pend_v1;
-        pend_old1 = second ? old : pend_old1;
-        ++pend_n;
-    };
-
-    // Sum cursor: the item summed next (its global item and tile).
-    int sk = 0, sgi = first_item, stile = first_tile;
-    float acc = 0.0f;
-
-    // Item k: item k + 2 is loaded, the next item's tables are built into
-    // the other buffer (their stores need no wait before this item's
-    // lookups, which read the other buffer), then this item's lookups are
-    // issued and summed.
-    auto step = [&](const uint32_t (&wk)[kBlockWords], const RowTaskX<T> &xnext, uint32_t (&wdst)[kBlockWords],
-                    RowTaskX<T> &xdst) __attribute__((always_inline)) {
-        if (sk + 2 < cnt) load_item(wdst, xdst);
-        const int parity = sk & 1;
-        if (sk + 1 < cnt) row_build_tables<T>(&tables[wave][parity ^ 1][0], xnext, lane);
-        RowLookups look;
-        row_lookups(look, wk, lds, table_base0 + static_cast<uint32_t>(parity * kRowTableFloats * 4));
-        const float sum = row_sum(look);
-        const float scale = half_bits_to_float(wk[0]);
-        acc = fmaf(scale, sum, acc);
-        // Next item: a new tile starts when the group wraps or run B begins.
-        ++sk;
-        ++sgi;
-        const bool run_switch = sk == len_a;
-        if (sk < cnt && (run_switch || sgi - stile * G == G)) {
-            contribute(stile, acc);
-            acc = 0.0f;
-            if (run_switch) sgi = b0;
-            stile = sgi / G;
-        }
-    };
-
-    if (cnt > 0) {
-        // Item 0's tables, then three items per trip with static register
-        // roles (words w0/w1/w2 and task activations x0/x1/x2 rotate).
-        row_build_tables<T>(&tables[wave][0][0], x0, lane);
-        for (int k0 = 0; k0 < cnt; k0 += 3) {
-            step(w0, x1, w2, x2);
-            if (k0 == 0) TQ1_PHASE(row_wave_id, 2);  // first item summed
-            if (k0 + 1 >= cnt) break;
-            step(w1, x2, w0, x0);
-            if (k0 + 2 >= cnt) break;
-            step(w2, x0, w1, x1);
-        }
-        TQ1_PHASE(row_wave_id, 3);  // all items summed
-        contribute(stile, acc);
-        if (pend_n > 0) {
-            const bool A = pend_q0 == qa;
-            row_reduce<T, GLU>(y, geo, legacy_counters, row_counters, row_slots, b, pend_q0, rem_tile0 + pend_q0,
-                               A ? a_lo : z_lo, A ? a_hi : z_hi, A ? a_slot : z_slot, pend_v0, pend_old0);
-        }
-        if (pend_n > 1) {
-            const bool A = pend_q1 == qa;
-            row_reduce<T, GLU>(y, geo, legacy_counters, row_counters, row_slots, b, pend_q1, rem_tile0 + pend_q1,
-                               A ? a_lo : z_lo, A ? a_hi : z_hi, A ? a_slot : z_slot, pend_v1, pend_old1);
-        }
+        strip_store<T, GLU>(y, lo + lane, lane, lane < R, total);
     }
-    TQ1_PHASE(row_wave_id, 4);  // done
+    TQ1_PHASE(strip_wave_id, 4);  // done
 }
 
 // The elementwise SwiGLU step over a linear's output whose rows alternate
@@ -2887,11 +2617,8 @@ static_assert(kCounterRegionBytes == kWorkspaceCounterBytes, "one counter region
 constexpr int kErrorSlot = kCounterSlots - 1;
 static_assert(kErrorSlot == kWorkspaceErrorSlot, "one error word");
 constexpr int kUsableCounters = kCounterSlots - 16;
-// Then the M = 1 row GEMV's counters and piece slots (row_gemv_kernel), also
-// zero between calls, and never written by any other kernel.
-constexpr size_t kRowRegionOffset = kCounterRegionBytes;
 // Partials of every split kernel start here.
-constexpr size_t kPartialOffset = kRowRegionOffset + kRowRegionBytes;
+constexpr size_t kPartialOffset = kCounterRegionBytes;
 
 struct LutPlan {
     int batch_tile;
@@ -3095,55 +2822,65 @@ int launch_lut_once(const uint32_t *packed, const void *x, void *y, int64_t M, i
     return fail(TERNEL_TQ1_EINVAL, "no LUT23 kernel for chunk %d, batch tile %d", plan.chunk, plan.batch_tile);
 }
 
-// The M = 1 row GEMV (row_gemv_kernel): one workgroup per CU (at most one
-// per item), F whole tiles each and the R leftover tiles dealt out in runs.
-struct RowPlan {
-    RowGeometry geo;
-    size_t workspace_bytes;  // the zero regions when leftover tiles exist, else 0
-};
-
-int plan_row(int64_t rows, int64_t columns, RowPlan *plan) {
-    const int64_t T = ceil_div(rows, kTileRows);
+// The M = 1 strip GEMV (strip_gemv_kernel): one workgroup per CU, at most
+// one per two rows, for strips below 64 rows and at most 40 groups.
+int plan_strip(int64_t rows, int64_t columns, StripGeometry *geo) {
     const int64_t G = columns / kBlockWeights;
-    int64_t P = std::min<int64_t>(device_cu_count(), kRowMaxWorkgroups);
-    if (P > T * G) P = T * G;
-    if (P < 1) P = 1;
-    const int64_t F = T / P;
-    if (T * G > INT32_MAX / kRowWaves)
-        return fail(TERNEL_TQ1_EINVAL, "tensor too large for the row GEMV's 32-bit item indices");
-    RowGeometry &geo = plan->geo;
-    geo.N = static_cast<int>(rows);
-    geo.G = static_cast<int>(G);
-    geo.full = static_cast<int>(F);
-    geo.rem_tiles = static_cast<int>(T - P * F);
-    geo.P = static_cast<int>(P);
-    geo.Pr = static_cast<int>(std::min<int64_t>(P, (T - P * F) * G));
-    geo.spin_limit = g_spin_limit.load();
-    plan->workspace_bytes = geo.rem_tiles > 0 ? kPartialOffset : 0;
+    if (G > kStripMaxGroups) return fail(TERNEL_TQ1_EINVAL, "the strip GEMV takes at most %d groups per row", kStripMaxGroups);
+    const int64_t units = (rows + 1) / 2;
+    const int64_t P = std::max<int64_t>(1, std::min<int64_t>(device_cu_count(), units));
+    if (2 * ceil_div(units, P) > kStripMaxRows)
+        return fail(TERNEL_TQ1_EINVAL, "strips of %lld rows are past the strip GEMV's %d",
+                    static_cast<long long>(2 * ceil_div(units, P)), kStripMaxRows);
+    if (P * units > INT32_MAX || rows * G * kBlockWords > INT32_MAX)
+        return fail(TERNEL_TQ1_EINVAL, "tensor too large for the strip GEMV's 32-bit indices");
+    geo->N = static_cast<int>(rows);
+    geo->G = static_cast<int>(G);
+    geo->P = static_cast<int>(P);
+    geo->units = static_cast<int>(units);
+    geo->value_base = static_cast<int>((G * kLutFloats + 3) / 4 * 4);
     return TERNEL_TQ1_OK;
 }
 
 template <typename T>
-int launch_row(const uint32_t *packed, const void *x, void *y, const RowPlan &plan, void *ws, hipStream_t stream,
-               bool glu) {
-    unsigned *legacy = static_cast<unsigned *>(ws);
-    unsigned *counters = ws ? reinterpret_cast<unsigned *>(static_cast<char *>(ws) + kRowRegionOffset) : nullptr;
-    unsigned long long *slots =
-        ws ? reinterpret_cast<unsigned long long *>(static_cast<char *>(ws) + kRowRegionOffset + kRowCounterBytes)
-           : nullptr;
-    const dim3 grid(static_cast<unsigned>(plan.geo.P));
-    if (glu)
-        hipLaunchKernelGGL((row_gemv_kernel<T, true>), grid, dim3(kRowThreads), 0, stream, packed,
-                           static_cast<const T *>(x), static_cast<T *>(y), legacy, counters, slots, plan.geo);
-    else
-        hipLaunchKernelGGL((row_gemv_kernel<T, false>), grid, dim3(kRowThreads), 0, stream, packed,
-                           static_cast<const T *>(x), static_cast<T *>(y), legacy, counters, slots, plan.geo);
+int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeometry &geo, hipStream_t stream,
+                 bool glu) {
+    const dim3 grid(static_cast<unsigned>(geo.P));
+    const bool stage = sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    const T *xt = static_cast<const T *>(x);
+    T *yt = static_cast<T *>(y);
+#define TQ1_STRIP_LAUNCH(STAGE)                                                                                   \
+    do {                                                                                                        \
+        if (glu)                                                                                                \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE>), grid, dim3(kStripThreads), 0, stream, packed, \
+                               xt, yt, geo);                                                                   \
+        else                                                                                                    \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE>), grid, dim3(kStripThreads), 0, stream,       \
+                               packed, xt, yt, geo);                                                           \
+    } while (0)
+    if constexpr (sizeof(T) == 2) {
+        if (stage) {
+            TQ1_STRIP_LAUNCH(true);
+            TQ1_LAUNCH_CHECK();
+            return TERNEL_TQ1_OK;
+        }
+    }
+    TQ1_STRIP_LAUNCH(false);
+#undef TQ1_STRIP_LAUNCH
     TQ1_LAUNCH_CHECK();
     return TERNEL_TQ1_OK;
 }
 
-// The automatic configuration of one activation vector runs the row GEMV.
-bool uses_row_gemv(int64_t M, int batch_tile, int k_split) { return false && M == 1 && batch_tile == 0 && k_split == 0; }
+// The automatic configuration of one activation vector runs the strip GEMV
+// where it applies (the LUT23 kernel above otherwise).
+bool uses_strip_gemv(int64_t M, int batch_tile, int k_split, int64_t rows, int64_t columns) {
+    if (M != 1 || batch_tile != 0 || k_split != 0 || rows < kStripMinRows) return false;
+    StripGeometry geo;
+    const std::string saved = g_last_error;
+    const bool ok = plan_strip(rows, columns, &geo) == TERNEL_TQ1_OK;
+    snprintf(g_last_error, sizeof(g_last_error), "%s", saved.c_str());
+    return ok;
+}
 
 struct GemmPlan {
     int k_split;
@@ -3744,11 +3481,7 @@ int ternel_tq1_deinterleave(const uint32_t *packed, int64_t rows, int64_t column
 
 size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
-    if (uses_row_gemv(M, batch_tile, k_split)) {
-        RowPlan row;
-        if (plan_row(rows, columns, &row) != TERNEL_TQ1_OK) return 0;
-        return row.workspace_bytes;
-    }
+    if (uses_strip_gemv(M, batch_tile, k_split, rows, columns)) return 0;
     LutPlan plan;
     if (plan_lut(M, rows, columns, batch_tile, k_split, &plan) != TERNEL_TQ1_OK) return 0;
     return plan.counter_bytes + plan.partial_bytes;
@@ -3760,22 +3493,19 @@ int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M,
     int rc;
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
-    if (uses_row_gemv(M, batch_tile, k_split)) {
-        RowPlan row;
-        if ((rc = plan_row(rows, columns, &row)) != TERNEL_TQ1_OK) return rc;
+    if (uses_strip_gemv(M, batch_tile, k_split, rows, columns)) {
+        StripGeometry geo;
+        if ((rc = plan_strip(rows, columns, &geo)) != TERNEL_TQ1_OK) return rc;
         if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
         if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
-        if (row.workspace_bytes && (!ws || ws_bytes < row.workspace_bytes))
-            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the row GEMV needs",
-                        ws_bytes, row.workspace_bytes);
         hipStream_t s = static_cast<hipStream_t>(stream);
         switch (dtype) {
             case TERNEL_TQ1_F16:
-                return launch_row<_Float16>(packed, x, y, row, ws, s, false);
+                return launch_strip<_Float16>(packed, x, y, geo, s, false);
             case TERNEL_TQ1_BF16:
-                return launch_row<bf16_t>(packed, x, y, row, ws, s, false);
+                return launch_strip<bf16_t>(packed, x, y, geo, s, false);
             default:
-                return launch_row<float>(packed, x, y, row, ws, s, false);
+                return launch_strip<float>(packed, x, y, geo, s, false);
         }
     }
     LutPlan plan;
@@ -3803,6 +3533,22 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
     int rc;
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
+    if (uses_strip_gemv(M, batch_tile, k_split, rows, columns)) {
+        // the same kernel as ternel_tq1_matmul, which takes no workspace
+        StripGeometry geo;
+        if ((rc = plan_strip(rows, columns, &geo)) != TERNEL_TQ1_OK) return rc;
+        if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
+        if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        switch (dtype) {
+            case TERNEL_TQ1_F16:
+                return launch_strip<_Float16>(packed, x, y, geo, s, false);
+            case TERNEL_TQ1_BF16:
+                return launch_strip<bf16_t>(packed, x, y, geo, s, false);
+            default:
+                return launch_strip<float>(packed, x, y, geo, s, false);
+        }
+    }
     LutPlan plan;
     if ((rc = plan_lut(M, rows, columns, batch_tile, k_split, &plan, kNoAllocPartialBytes)) != TERNEL_TQ1_OK)
         return rc;
@@ -3946,7 +3692,7 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
 size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK || rows % 2) return 0;
     if (linear_uses_lut(M, rows, columns, dtype))
-        return ternel_tq1_matmul_workspace_bytes(M, rows, columns, uses_row_gemv(M, 0, 0) ? 0 : 1, 0);
+        return ternel_tq1_matmul_workspace_bytes(M, rows, columns, uses_strip_gemv(M, 0, 0, rows, columns) ? 0 : 1, 0);
     return swiglu_pairs_offset(M, rows, columns) + static_cast<size_t>(M) * rows * sizeof(_Float16);
 }
 
@@ -3962,19 +3708,16 @@ int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M,
     if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
     if (!x || !z) return fail(TERNEL_TQ1_EINVAL, "null pointer");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (linear_uses_lut(M, rows, columns, dtype) && uses_row_gemv(M, 0, 0)) {
-        RowPlan row;
-        if ((rc = plan_row(rows, columns, &row)) != TERNEL_TQ1_OK) return rc;
-        if (row.workspace_bytes && (!ws || ws_bytes < row.workspace_bytes))
-            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the row GEMV needs",
-                        ws_bytes, row.workspace_bytes);
+    if (linear_uses_lut(M, rows, columns, dtype) && uses_strip_gemv(M, 0, 0, rows, columns)) {
+        StripGeometry geo;
+        if ((rc = plan_strip(rows, columns, &geo)) != TERNEL_TQ1_OK) return rc;
         switch (dtype) {
             case TERNEL_TQ1_F16:
-                return launch_row<_Float16>(packed, x, z, row, ws, s, true);
+                return launch_strip<_Float16>(packed, x, z, geo, s, true);
             case TERNEL_TQ1_BF16:
-                return launch_row<bf16_t>(packed, x, z, row, ws, s, true);
+                return launch_strip<bf16_t>(packed, x, z, geo, s, true);
             default:
-                return launch_row<float>(packed, x, z, row, ws, s, true);
+                return launch_strip<float>(packed, x, z, geo, s, true);
         }
     }
     if (linear_uses_lut(M, rows, columns, dtype)) {

@@ -1,0 +1,129 @@
+"""The strip GEMV (one activation vector, strips of at most 62 rows per CU, at
+most 40 groups per row) against the oracle.
+
+The automatic configuration of ``tq1_matmul_words`` runs it for these shapes;
+each test first checks, through the workspace query (the strip GEMV needs
+none, the LUT23 kernel a split-K workspace), that the shape does take it.
+Covered: staged fp16/bf16 activations, fp32 and unaligned fp16 activations
+(read from global memory), strips of unequal and odd row counts, one group per
+row, the 62-row edge, the fused SwiGLU form, exact integer arithmetic on every
+code byte and tail byte, and run-to-run bit identity.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tq1_oracle as O
+from tests.gpu_util import layout, pack, random_blocks, to_dev
+from tests.test_gpu_swiglu import spacing
+from ternel_amd import _lib
+from ternel_amd.kernels import MatmulConfig, tq1_matmul_words, tq1_swiglu_words
+
+pytestmark = pytest.mark.gpu
+
+ORACLE_TOLERANCE = 1e-5      # src/ternel_mlx/kernel_gate.py:105 (fp32 output)
+NORTH_STAR_TOLERANCE = 1e-3  # BASELINE.json north star (fp16 output)
+BF16_TOLERANCE = 1e-2        # src/ternel_mlx/kernel_gate.py:113 (bf16 output: 8-bit significand)
+TOLERANCE = {torch.float32: ORACLE_TOLERANCE, torch.float16: NORTH_STAR_TOLERANCE, torch.bfloat16: BF16_TOLERANCE}
+
+
+def takes_strip(rows: int, columns: int) -> bool:
+    return _lib.lib().ternel_tq1_matmul_workspace_bytes(1, rows, columns, 0, 0) == 0
+
+
+def run(blocks: np.ndarray, x: torch.Tensor) -> torch.Tensor:
+    rows, g, _ = blocks.shape
+    assert takes_strip(rows, g * 128), f"{rows}x{g * 128} does not take the strip GEMV on this device"
+    out = tq1_matmul_words(pack(blocks), x, layout=layout(rows, g * 128), config=MatmulConfig())
+    torch.cuda.synchronize()
+    return out
+
+
+# (rows, columns): QKV; 4096^2; one group; strips of 8 and 10 rows (2050 rows
+# over 256 CUs) and an odd last strip; the 62-row edge (15872 rows); 12 groups.
+SHAPES = ((8192, 5120), (4096, 4096), (2048, 128), (2050, 640), (3001, 1024), (15872, 5120), (6144, 1536))
+
+
+@pytest.mark.parametrize(("rows", "columns"), SHAPES)
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+def test_strip_gemv_matches_the_oracle(rows, columns, dtype) -> None:
+    print(f"strip: rows={rows} columns={columns} {dtype}", flush=True)
+    blocks = random_blocks(rows, columns, seed=rows * 7 + columns)
+    x = np.random.default_rng(rows + columns).normal(0.0, 1.0, size=(1, columns)).astype(np.float32)
+    xd = to_dev(x).to(dtype)
+    got = run(blocks, xd).float().cpu().numpy()
+    oracle = O.oracle_matmul(blocks, xd.float().cpu().numpy().astype(np.float64), rows=rows, columns=columns)
+    assert O.compare(got, oracle)["normalised_max_abs_error"] < TOLERANCE[dtype]
+
+
+def test_unaligned_fp16_activations_are_read_from_global_memory() -> None:
+    rows, columns = 8192, 5120
+    blocks = random_blocks(rows, columns, seed=17)
+    x = np.random.default_rng(17).normal(0.0, 1.0, size=(1, columns)).astype(np.float16)
+    storage = torch.zeros(columns + 8, dtype=torch.float16, device="cuda")
+    view = storage[3:3 + columns].view(1, columns)
+    view.copy_(to_dev(x))
+    assert view.data_ptr() % 16 != 0
+    got = run(blocks, view)
+    aligned = run(blocks, to_dev(x))
+    # the same tables and sums either way
+    assert torch.equal(got.view(torch.int16), aligned.view(torch.int16))
+    oracle = O.oracle_matmul(blocks, x.astype(np.float64), rows=rows, columns=columns)
+    assert O.compare(got.float().cpu().numpy(), oracle)["normalised_max_abs_error"] < NORTH_STAR_TOLERANCE
+
+
+def test_every_code_byte_and_tail_byte_is_exact() -> None:
+    """Row p (of 2187 = 9 x 243) holds byte p % 243 in every one of its 25
+    slots of group s = slot, and tail byte p % 27; x carries 1, 3, 9, 27, 81 in
+    slot s of group s (and 1, 3, 9 in the tail of group 0), so row p is
+    25 (p % 243 - 121) + (p % 27 - 13), exact in fp32."""
+    rows, groups = 2187, 25
+    blocks = np.zeros((rows, groups, 28), dtype=np.uint8)
+    blocks[:, :, 0], blocks[:, :, 1] = 0x00, 0x3C  # scale 1.0
+    p = np.arange(rows)
+    blocks[:, :, 2:27] = (p % 243)[:, None, None]
+    blocks[:, :, 27] = (p % 27)[:, None]
+    x = np.zeros((1, groups * 128), dtype=np.float32)
+    for s in range(groups):
+        x[0, s * 128 + 5 * s: s * 128 + 5 * s + 5] = (1, 3, 9, 27, 81)
+    x[0, 125:128] = (1, 3, 9)
+    got = run(blocks, to_dev(x)).cpu().numpy()[0]
+    want = 25.0 * (p % 243 - 121) + (p % 27 - 13)
+    np.testing.assert_array_equal(got, want.astype(np.float32))
+
+
+def test_results_are_bit_identical_from_run_to_run() -> None:
+    rows, columns = 8192, 5120
+    blocks = random_blocks(rows, columns, seed=5)
+    packed = pack(blocks)
+    x = to_dev(np.random.default_rng(5).normal(0.0, 1.0, size=(1, columns)).astype(np.float16))
+    assert takes_strip(rows, columns)
+    outs = [tq1_matmul_words(packed, x, layout=layout(rows, columns), config=MatmulConfig()) for _ in range(4)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_fused_swiglu_form(dtype) -> None:
+    """Rows alternate gate, up (12288 rows: 6144 units); the kernel writes
+    SiLU(gate) * up from the two outputs rounded to the activation type."""
+    rows, columns = 12288, 5120
+    assert takes_strip(rows, columns)
+    blocks = random_blocks(rows, columns, seed=23)
+    x = to_dev(np.random.default_rng(23).normal(0.0, 1.0, size=(1, columns)).astype(np.float32)).to(dtype)
+    z = tq1_swiglu_words(pack(blocks), x, layout=layout(rows, columns))
+    linear = tq1_matmul_words(pack(blocks), x, layout=layout(rows, columns), config=MatmulConfig())
+    torch.cuda.synchronize()
+    gate, up = linear[:, 0::2].float(), linear[:, 1::2].float()
+    want = (gate / (1.0 + torch.exp(-gate)) * up).to(dtype).float()
+    got = z.float()
+    # one step of the activation type apart at most (the kernel's expf vs torch.exp)
+    assert bool(((got - want).abs() <= spacing(want, dtype)).all())
+    oracle = O.oracle_matmul(blocks, x.float().cpu().numpy().astype(np.float64), rows=rows, columns=columns)
+    g64, u64 = oracle[:, 0::2], oracle[:, 1::2]
+    ref = g64 / (1.0 + np.exp(-g64)) * u64
+    assert O.compare(got.cpu().numpy(), ref)["normalised_max_abs_error"] < 4 * TOLERANCE[dtype]
