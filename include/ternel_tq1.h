@@ -43,9 +43,11 @@
  * zero-filled workspace can serve calls of any shape (the reference's
  * stream-K contract, cuda/tq1_lut23_streamk.cu:320-334). Calls sharing one
  * workspace must not overlap in time (one workspace per stream). A kernel
- * whose bounded wait for another workgroup's published partial gives up sets
- * the error word (ternel_tq1_workspace_error) and may leave counters set: zero
- * the workspace again before reusing it.
+ * whose bounded wait for another workgroup's published partial gives up
+ * writes its tile as NaN (it sums nothing), sets the error word
+ * (ternel_tq1_workspace_error) and may leave counters set; a launch that
+ * finds the word set writes every tile needing the counters as NaN without
+ * touching them. Zero the workspace again before reusing it.
  */
 #ifndef TERNEL_TQ1_H
 #define TERNEL_TQ1_H
@@ -269,11 +271,11 @@ size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t column
 /*
  * Reads a workspace's error word (synchronises `stream`): *error = 0, or a
  * bitmask of the kernels whose bounded wait for a published partial gave up
- * (2 = the wide GEMM's stream-K reduction; the LUT23 and direct-form
- * fix-ups never wait). No
- * counterpart in the reference, whose fix-ups (cuda/tq1_lut23_streamk.cu:
- * 194-256) spin without a bound; here a wait that cannot complete is reported
- * instead of hanging the device or summing unpublished data.
+ * (the value 2 = the wide GEMM's stream-K reduction; the LUT23 and
+ * direct-form fix-ups never wait). No counterpart in the reference, whose
+ * fix-ups (cuda/tq1_lut23_streamk.cu:194-256) spin without a bound; here a
+ * wait that cannot complete writes NaN tiles and is reported instead of
+ * hanging the device or summing unpublished data.
  */
 int ternel_tq1_workspace_error(const void *ws, size_t ws_bytes, int *error, void *stream);
 

@@ -67,6 +67,8 @@ constexpr int kThreads = 256;
 // error word (the host section keeps every kernel's counters below it).
 constexpr int kWorkspaceCounterBytes = 64 * 1024;
 constexpr int kWorkspaceErrorSlot = kWorkspaceCounterBytes / 4 - 1;
+// Read in place of the error word by launches that have no workspace.
+__device__ const unsigned kZeroWord = 0;
 
 // Phase timestamps (built only with -DTERNEL_TQ1_PROFILE, into a separate
 // library that bench.py --phase-profile loads): lane 0 of each wave of the
@@ -2058,6 +2060,14 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     (void)wide_wave_id;
     TQ1_PHASE(wide_wave_id, 0);
     TQ1_PHASE_XCC(wide_wave_id);
+    // The workspace's error word as this launch finds it (read by every
+    // thread, from a zero word when there is no workspace, so no load sits
+    // behind a branch). Set, an earlier reduction gave up and the counters
+    // may be stale: every tile split over workgroups is written as NaN
+    // without touching them, until the host zeroes the workspace.
+    const unsigned refused =
+        __hip_atomic_load(counters ? counters + kWorkspaceErrorSlot : &kZeroWord, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
     if (u_begin >= u_end) return;
     const int last_u = u_end - 1;
 
@@ -2329,6 +2339,13 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             }
         }
     };
+    auto store_nan_tile = [&](int t) {
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = __builtin_nanf("");
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) store_frag(t, nb, v);
+    };
     // Stream-K reduction. A tile split over workgroups q0..q1 is summed in
     // workgroup order by the last of them to arrive (counters[t] counts
     // arrivals), from its own accumulators and the partials the others stored
@@ -2366,10 +2383,17 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         }
         const int q0 = wide_owner(geo.units, tu0, P), q1 = wide_owner(geo.units, tu1 - 1, P);
         if (tid == 0)
-            s_last = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                     static_cast<unsigned>(q1 - q0);
+            s_last = refused ? 2u
+                             : (__hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                                        static_cast<unsigned>(q1 - q0)
+                                    ? 1u
+                                    : 0u);
         __syncthreads();
         TQ1_PHASE(wide_wave_id, 6);
+        if (s_last == 2u) {
+            store_nan_tile(t);
+            return;
+        }
         if (!s_last) {
             const int base = slot_base(p, seg_begin == u_begin ? 0 : 1);
 #pragma unroll
@@ -2384,9 +2408,10 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             return;
         }
         // Last to arrive: wait (bounded) until the others' partials are published.
-        // A wait that gives up sets the workspace error word and leaves both
-        // counters as they are -- a late publication must not carry into the
-        // next call; the host re-zeroes the workspace after reading the error.
+        // A wait that gives up writes the tile as NaN (it sums nothing), sets
+        // the workspace error word and leaves both counters as they are: a
+        // late publication cannot carry into the next call, which finds the
+        // word set and refuses; the host zeroes the workspace after reading it.
         if (tid == 0) {
             bool published = false;
             for (int spin = 0; spin <= geo.spin_limit; ++spin) {
@@ -2403,7 +2428,10 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
         }
         __syncthreads();
         TQ1_PHASE(wide_wave_id, 7);
-        const bool published = s_published;
+        if (!s_published) {
+            store_nan_tile(t);
+            return;
+        }
         // The sum runs in workgroup order q0..q1: the partials of q0..p-1, this
         // workgroup's accumulators, then the partials of p+1..q1. It is formed
         // in place in acc -- (prefix) + acc equals acc + (prefix) exactly in
@@ -2461,7 +2489,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                 store_frag(t, nb0 + i, out);
             }
         }
-        if (tid == 0 && published) {
+        if (tid == 0) {
             __hip_atomic_store(counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(counters + kWideTileSlots + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

@@ -84,6 +84,8 @@ class MatmulConfig:
 
 GEMM_FORMS = {"auto": 0, "tile": 1, "direct": 2, "wide": 3}
 DIRECT_MAX_BATCH = 64
+# The automatic GEMM form may be the wide one above this many activation rows.
+WIDE_MIN_AUTO_BATCH = 32
 
 
 @dataclass(frozen=True)
@@ -258,6 +260,68 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     return buf
 
 
+# Launches that may give up a bounded wait (the wide form's stream-K
+# reduction) leave an event per workspace; the next call on the device reads
+# the error word of every workspace whose event has completed -- no wait on
+# the caller's stream, a 4-byte copy on a side stream -- and raises
+# ``NativeError`` if it is set, after zeroing that workspace. (The kernels
+# themselves refuse a workspace whose word is set: they write the tiles that
+# would need its counters as NaN.) Graph replays are not watched; a caller
+# replaying graphs runs ``check_workspaces()`` at its own sync points.
+_WATCH: dict[tuple[int, int], torch.cuda.Event] = {}
+_SIDE: dict[int, torch.cuda.Stream] = {}
+_ERROR_WORD_OFFSET = 64 * 1024 - 4  # the last word of the 64 KiB counter region
+
+
+def _key_of(buf: torch.Tensor) -> tuple[int, int] | None:
+    for key, b in _WORKSPACES.items():
+        if b is buf:
+            return key
+    return None
+
+
+def _watch(ws: torch.Tensor | None, may_give_up: bool) -> None:
+    """After a launch: remember to read ``ws``'s error word once it is done."""
+    if ws is None or not may_give_up or torch.cuda.is_current_stream_capturing():
+        return
+    key = _key_of(ws)
+    if key is None:
+        return
+    event = torch.cuda.Event()
+    event.record(torch.cuda.current_stream(ws.device))
+    _WATCH[key] = event
+
+
+def _surface(device: torch.device) -> None:
+    """Before a launch: raise if a watched workspace of ``device`` reported a
+    wait that gave up (zeroing it first, so the next call starts clean)."""
+    if not _WATCH or torch.cuda.is_current_stream_capturing():
+        return
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    failed = {}
+    for key, event in list(_WATCH.items()):
+        if key[0] != index or not event.query():
+            continue
+        del _WATCH[key]
+        buf = _WORKSPACES[key]
+        side = _SIDE.get(index)
+        if side is None:
+            side = _SIDE[index] = torch.cuda.Stream(device=buf.device)
+        word = torch.empty(4, dtype=torch.uint8, pin_memory=True)
+        with torch.cuda.stream(side):
+            side.wait_event(event)
+            word.copy_(buf[_ERROR_WORD_OFFSET:_ERROR_WORD_OFFSET + 4], non_blocking=True)
+        side.synchronize()
+        value = int(word.view(torch.int32).item())
+        if value:
+            buf.zero_()
+            failed[key] = value
+    if failed:
+        torch.cuda.synchronize(index)
+        raise _lib.NativeError(f"a kernel's bounded wait for a published partial gave up: {failed}; "
+                               "its tiles were written as NaN and the workspace has been zeroed")
+
+
 def workspace_errors() -> dict[tuple[int, int], int]:
     """The error word of every workspace (synchronises each one's stream): a
     nonzero word names the kernels whose bounded wait for another workgroup's
@@ -278,6 +342,7 @@ def check_workspaces() -> None:
     workspace is zeroed again first (its counters may be left set), so the
     next call starts clean."""
     failed = {key: word for key, word in workspace_errors().items() if word}
+    _WATCH.clear()
     for key in failed:
         _WORKSPACES[key].zero_()
     if failed:
@@ -332,6 +397,7 @@ def tq1_gemm_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTenso
         raise FormatError(f"the direct-fragment form takes at most {DIRECT_MAX_BATCH} activation rows, got {batch}")
     form = GEMM_FORMS[form_name]
     x = _aligned_rows(x)
+    _surface(x.device)
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     need = handle.ternel_tq1_gemm_workspace_bytes(batch, layout.rows, layout.columns, form, config.k_split)
@@ -340,6 +406,7 @@ def tq1_gemm_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTenso
         packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns,
         _lib.DTYPE_F16, form, config.k_split, ws.data_ptr() if ws is not None else None,
         ws.numel() if ws is not None else 0, _stream(x.device)))
+    _watch(ws, form_name == "wide" or (form_name == "auto" and batch > WIDE_MIN_AUTO_BATCH))
     return out
 
 
@@ -348,6 +415,7 @@ def tq1_linear_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTen
     check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
     x = _aligned_rows(x)
+    _surface(x.device)
     out = torch.empty((batch, layout.rows), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     code = _DTYPE_CODE[x.dtype]
@@ -356,6 +424,7 @@ def tq1_linear_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTen
     _lib.check(handle.ternel_tq1_linear(
         packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns, code,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(x.device)))
+    _watch(ws, handle.ternel_tq1_linear_kernel(batch, layout.rows, layout.columns, code) == GEMM_FORMS["wide"])
     return out
 
 
@@ -370,6 +439,7 @@ def tq1_swiglu_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTen
         raise FormatError(f"a SwiGLU weight interleaves gate and up rows, so its rows must be even, "
                           f"got {layout.rows}")
     x = _aligned_rows(x)
+    _surface(x.device)
     out = torch.empty((batch, layout.rows // 2), dtype=x.dtype, device=x.device)
     handle = _lib.lib()
     code = _DTYPE_CODE[x.dtype]
@@ -378,6 +448,7 @@ def tq1_swiglu_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTen
     _lib.check(handle.ternel_tq1_swiglu(
         packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns, code,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(x.device)))
+    _watch(ws, handle.ternel_tq1_linear_kernel(batch, layout.rows, layout.columns, code) == GEMM_FORMS["wide"])
     return out
 
 

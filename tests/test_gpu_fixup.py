@@ -121,32 +121,75 @@ def test_split_gemv_on_two_streams_at_once() -> None:
     check_workspaces()
 
 
-def _forced_give_up(run) -> int:
-    handle = _lib.lib()
-    run()  # sizes the workspace eagerly
-    torch.cuda.synchronize()
-    old = handle.ternel_tq1_set_spin_limit(-1)
-    try:
-        run()
-        torch.cuda.synchronize()
-    finally:
-        handle.ternel_tq1_set_spin_limit(old)
-    words = [w for w in workspace_errors().values() if w]
-    with pytest.raises(_lib.NativeError, match="bounded wait"):
-        check_workspaces()
-    assert not any(workspace_errors().values())  # check_workspaces zeroed it again
-    return words[0] if words else 0
-
-
-def test_a_wide_reduction_that_gives_up_is_reported_and_the_next_call_is_clean() -> None:
+def _wide_case():
     rows, columns, batch = 17408, 5120, 512
     blocks = random_blocks(rows, columns, seed=43)
     x = np.random.default_rng(43).normal(0, 0.5, size=(batch, columns)).astype(np.float16)
     packed, xt, lay = pack(blocks), to_dev(x), layout(rows, columns)
     config = GemmConfig(form="wide")
-    want = tq1_gemm_words(packed, xt, layout=lay, config=config).cpu()
-    assert _forced_give_up(lambda: tq1_gemm_words(packed, xt, layout=lay, config=config)) & 2
+    want = tq1_gemm_words(packed, xt, layout=lay, config=config)  # also sizes the workspace eagerly
+    torch.cuda.synchronize()
+    return packed, xt, lay, config, want.cpu()
+
+
+def _nan_tiles_and_exact_elsewhere(got: torch.Tensor, want: torch.Tensor) -> None:
+    """The tiles whose reduction gave up (or was refused) are NaN, whole
+    32-row x 256-column tiles of the wide form; every other value is the
+    exact result -- nothing finite and wrong."""
+    nan = torch.isnan(got.float())
+    assert nan.any()
+    assert torch.equal(got[~nan], want[~nan])
+    m, n = got.shape
+    tiles = nan[: m // 32 * 32, : n // 256 * 256].reshape(m // 32, 32, n // 256, 256)
+    assert bool((tiles.all(dim=3).all(dim=1) == tiles.any(dim=3).any(dim=1)).all())
+
+
+def test_a_wide_reduction_that_gives_up_writes_nan_tiles_and_the_next_call_raises() -> None:
+    packed, xt, lay, config, want = _wide_case()
+    handle = _lib.lib()
+    # A negative limit makes every bounded wait give up at once (host-driven:
+    # every kernel still exits normally; the other contributors publish late).
+    old = handle.ternel_tq1_set_spin_limit(-1)
+    try:
+        got = tq1_gemm_words(packed, xt, layout=lay, config=config)
+        torch.cuda.synchronize()
+    finally:
+        handle.ternel_tq1_set_spin_limit(old)
+    _nan_tiles_and_exact_elsewhere(got.cpu(), want)
+    assert any(w & 2 for w in workspace_errors().values())
+    # The next call on that workspace raises before launching, and zeroes it.
+    with pytest.raises(_lib.NativeError, match="bounded wait"):
+        tq1_gemm_words(packed, xt, layout=lay, config=config)
+    assert not any(workspace_errors().values())
     assert torch.equal(tq1_gemm_words(packed, xt, layout=lay, config=config).cpu(), want)
+
+
+def test_a_workspace_whose_error_word_is_set_is_refused_by_the_kernel() -> None:
+    """Called through the C ABI (no host-side check), a launch on a workspace
+    left with its error word set -- stale counters -- writes the tiles that
+    need them as NaN and leaves every other tile exact."""
+    packed, xt, lay, config, want = _wide_case()
+    handle = _lib.lib()
+    rows, columns = lay.rows, lay.columns
+    batch = xt.shape[0]
+    need = handle.ternel_tq1_gemm_workspace_bytes(batch, rows, columns, 3, 0)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev())
+    ws[64 * 1024 - 4:64 * 1024].view(torch.int32).fill_(2)
+    out = torch.empty((batch, rows), dtype=torch.float16, device=dev())
+
+    def launch() -> None:
+        _lib.check(handle.ternel_tq1_gemm(packed.data_ptr(), xt.data_ptr(), out.data_ptr(), batch, rows, columns,
+                                          _lib.DTYPE_F16, 3, 0, ws.data_ptr(), ws.numel(),
+                                          torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+
+    launch()
+    _nan_tiles_and_exact_elsewhere(out.cpu(), want)
+    assert ws[: 64 * 1024 - 4].view(torch.int32).eq(0).all()  # no counter was touched
+    ws.zero_()
+    launch()
+    assert torch.equal(out.cpu(), want)
+    assert ws[: 64 * 1024].eq(0).all()  # counters back at zero (the partial slots keep data)
 
 
 def test_workspace_error_entry_refuses_a_workspace_without_an_error_word() -> None:
