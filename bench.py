@@ -506,6 +506,7 @@ def main() -> int:
     if not args.no_model_stream:
         result["model_stream"] = model_stream(torch, synthetic, pack_weights, tq1_matmul_words, tq1_get_rows_words, tq1_swiglu_words,
                                               PackedTensorLayout, MatmulConfig, graph_of, time_graph)
+        result["census_stream"] = census_stream(torch, synthetic, pack_weights, PackedTensorLayout, graph_of, time_graph)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
@@ -791,6 +792,101 @@ def model_stream(torch, synthetic, pack_weights, tq1_matmul_words, tq1_get_rows_
                               "GB/s": round(prefill_bytes / prefill_us / 1e3, 1),
                               "frac_of_hbm_peak": round(prefill_bytes / prefill_us / 1e3 / HBM_PEAK_GBS, 4),
                               "packed_table_us": round(from_packed_us, 2)},
+    }
+
+
+FULL_ATTENTION_INTERVAL = 4  # every fourth layer is full attention (the reference's tests/test_mlx_modules.py:71)
+
+
+def census_order() -> list:
+    """The 497 linear tensors of one decoded token in model order: 64 layers, a
+    full-attention layer (q, k, v, o) every fourth and linear attention (qkv,
+    z, a, b, out) in the others, each with its MLP (gate, up, down), then the
+    tied head -- the census of src/ternel_mlx/layout.py:179-195, whose
+    per-shape counts this order reproduces (checked below)."""
+    from ternel_amd.layout import DISPATCHES_PER_TOKEN, MODEL_LINEAR_SHAPES
+    order = []
+    for layer in range(C4_LAYERS):
+        if layer % FULL_ATTENTION_INTERVAL == FULL_ATTENTION_INTERVAL - 1:
+            order += [("self_attn.q_proj", 12288, 5120), ("self_attn.k_proj", 1024, 5120),
+                      ("self_attn.v_proj", 1024, 5120), ("self_attn.o_proj", 5120, 6144)]
+        else:
+            order += [("linear_attn.in_proj_qkv", 10240, 5120), ("linear_attn.in_proj_z", 6144, 5120),
+                      ("linear_attn.in_proj_a", 48, 5120), ("linear_attn.in_proj_b", 48, 5120),
+                      ("linear_attn.out_proj", 5120, 6144)]
+        order += [("mlp.gate_proj", 17408, 5120), ("mlp.up_proj", 17408, 5120), ("mlp.down_proj", 5120, 17408)]
+    order.append(("lm_head", HEAD_ROWS, 5120))
+    counts = {}
+    for _, rows, columns in order:
+        counts[(rows, columns)] = counts.get((rows, columns), 0) + 1
+    census = {(s.rows, s.columns): s.dispatches_per_token for s in MODEL_LINEAR_SHAPES}
+    if len(order) != DISPATCHES_PER_TOKEN or counts != census:
+        raise RuntimeError("the model order does not reproduce the 27B shape census")
+    return order
+
+
+def census_stream(torch, synthetic, pack_weights, PackedTensorLayout, graph_of, time_graph) -> dict:
+    """The reference's whole-model traversal (reports_v2/03_streaming_benchmark.md:5,10: 497 tensors,
+    5,604,802,560 packed bytes, 11.273 ms = 497.181 GB/s): every tensor once, in model order, as an
+    M=1 GEMV through the library's automatic configuration, each a distinct weight (5.6 GB, larger
+    than every cache). Each GEMV reads the previous one's output: two fp16 buffers alternate as
+    input and output (a GEMV with fewer outputs than the next one's columns leaves the rest of its
+    output buffer from earlier GEMVs), so no launch can start before the one it follows ends. One
+    HIP graph per traversal. Then every shape alone: its copies of the traversal in rotation."""
+    from ternel_amd import _lib
+    from ternel_amd.kernels import workspace
+    order = census_order()
+    handle = _lib.lib()
+    lays = [PackedTensorLayout.for_tensor(rows, columns) for _, rows, columns in order]
+    weights = [pack_weights(synthetic.device_blocks(rows, columns, seed=synthetic.SEED_BASE + 60 + i), layout=lay)
+               for i, ((_, rows, columns), lay) in enumerate(zip(order, lays))]
+    total = sum(packed_bytes(columns, rows) for _, rows, columns in order)
+    width = max(max(rows, columns) for _, rows, columns in order)
+    bufs = [synthetic.device_activations(1, width, seed=synthetic.SEED_BASE + 61 + i) for i in range(2)]
+    need = max(handle.ternel_tq1_matmul_workspace_bytes(1, rows, columns, 0, 0) for _, rows, columns in order)
+    ws = workspace(bufs[0].device, need)
+    ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+
+    def gemv(i: int, src, dst) -> None:
+        _, rows, columns = order[i]
+        _lib.check(handle.ternel_tq1_matmul(weights[i].data_ptr(), src.data_ptr(), dst.data_ptr(), 1, rows, columns,
+                                            _lib.DTYPE_F16, 0, 0, ws_ptr, ws_bytes,
+                                            torch.cuda.current_stream().cuda_stream))
+
+    def traversal() -> None:
+        for i in range(len(order)):
+            gemv(i, bufs[i % 2], bufs[(i + 1) % 2])
+
+    graph = graph_of(traversal)
+    time_graph(graph)  # a full warm-up traversal (the reference runs six)
+    ms = sorted(time_graph(graph) for _ in range(5))[2]  # median of five traversals
+    del graph
+    shapes = {}
+    for name, rows, columns in order:
+        key = f"{rows}x{columns}"
+        if key in shapes:
+            continue
+        idx = [i for i, (_, r, c) in enumerate(order) if (r, c) == (rows, columns)]
+        launches = max(len(idx), 16) if len(idx) > 1 else 8
+        g = graph_of(lambda idx=idx, launches=launches: [gemv(idx[s % len(idx)], bufs[0], bufs[1])
+                                                         for s in range(launches)])
+        us = sorted(time_graph(g) for _ in range(3))[1] / launches * 1e3
+        del g
+        nbytes = packed_bytes(columns, rows)
+        shapes[key] = {"tensor": name, "per_token": len(idx), "distinct_copies": len(idx), "us": round(us, 3),
+                       "GB/s": round(nbytes / us / 1e3, 1), "kernel": "strip" if handle.ternel_tq1_matmul_workspace_bytes(
+                           1, rows, columns, 0, 0) == 0 else "lut23"}
+    del weights, bufs
+    return {
+        "workload": "the reference's 497-tensor model-order traversal (27B census, src/ternel_mlx/layout.py:179-195): "
+                    "M=1 GEMVs, each reading the previous one's output, one HIP graph per traversal",
+        "tensors": len(order),
+        "packed_bytes": total,
+        "ms_per_traversal": round(ms, 4),
+        "GB/s": round(total / (ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "reference_GBs": 497.181,
+        "per_shape": shapes,
     }
 
 

@@ -67,8 +67,6 @@ constexpr int kThreads = 256;
 // error word (the host section keeps every kernel's counters below it).
 constexpr int kWorkspaceCounterBytes = 64 * 1024;
 constexpr int kWorkspaceErrorSlot = kWorkspaceCounterBytes / 4 - 1;
-// Read in place of the error word by launches that have no workspace.
-__device__ const unsigned kZeroWord = 0;
 
 // Phase timestamps (built only with -DTERNEL_TQ1_PROFILE, into a separate
 // library that bench.py --phase-profile loads): lane 0 of each wave of the
@@ -2060,14 +2058,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     (void)wide_wave_id;
     TQ1_PHASE(wide_wave_id, 0);
     TQ1_PHASE_XCC(wide_wave_id);
-    // The workspace's error word as this launch finds it (read by every
-    // thread, from a zero word when there is no workspace, so no load sits
-    // behind a branch). Set, an earlier reduction gave up and the counters
-    // may be stale: every tile split over workgroups is written as NaN
-    // without touching them, until the host zeroes the workspace.
-    const unsigned refused =
-        __hip_atomic_load(counters ? counters + kWorkspaceErrorSlot : &kZeroWord, __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
+
     if (u_begin >= u_end) return;
     const int last_u = u_end - 1;
 
@@ -2339,12 +2330,21 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             }
         }
     };
+    // Tile t as fp16 NaN (0x7e00), the rows store_frag writes.
     auto store_nan_tile = [&](int t) {
-        float v[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = __builtin_nanf("");
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) store_frag(t, nb, v);
+        const _Float16 nan16 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(0x7e00));
+#pragma unroll 1
+        for (int nb = 0; nb < NB; ++nb) {
+            const int m = (t / geo.tiles_n) * kCols + nb * 32 + (lane & 31);
+            if (m >= geo.M) continue;
+            _Float16 *yrow = y + static_cast<int64_t>(m) * geo.N;
+#pragma unroll 1
+            for (int run = 0; run < 2; ++run) {
+                const int n = (t % geo.tiles_n) * kWideRows + wave * 32 + 16 * run + (upper ? 8 : 0);
+                for (int e = 0; e < 8; ++e)
+                    if (n + e < geo.N) yrow[n + e] = nan16;
+            }
+        }
     };
     // Stream-K reduction. A tile split over workgroups q0..q1 is summed in
     // workgroup order by the last of them to arrive (counters[t] counts
@@ -2382,12 +2382,16 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             return;
         }
         const int q0 = wide_owner(geo.units, tu0, P), q1 = wide_owner(geo.units, tu1 - 1, P);
-        if (tid == 0)
-            s_last = refused ? 2u
-                             : (__hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                                        static_cast<unsigned>(q1 - q0)
-                                    ? 1u
-                                    : 0u);
+        // With the workspace's error word set (read beside the arrival, in
+        // flight at the same time), an earlier reduction gave up and the
+        // counters may be stale: every contributor writes the tile as NaN,
+        // until the host zeroes the workspace.
+        if (tid == 0) {
+            const unsigned word =
+                __hip_atomic_load(counters + kWorkspaceErrorSlot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned old = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = word ? 2u : (old == static_cast<unsigned>(q1 - q0) ? 1u : 0u);
+        }
         __syncthreads();
         TQ1_PHASE(wide_wave_id, 6);
         if (s_last == 2u) {

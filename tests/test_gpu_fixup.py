@@ -167,7 +167,8 @@ def test_a_wide_reduction_that_gives_up_writes_nan_tiles_and_the_next_call_raise
 def test_a_workspace_whose_error_word_is_set_is_refused_by_the_kernel() -> None:
     """Called through the C ABI (no host-side check), a launch on a workspace
     left with its error word set -- stale counters -- writes the tiles that
-    need them as NaN and leaves every other tile exact."""
+    need them as NaN and leaves every other tile exact, launch after launch,
+    until the workspace is zeroed."""
     packed, xt, lay, config, want = _wide_case()
     handle = _lib.lib()
     rows, columns = lay.rows, lay.columns
@@ -185,7 +186,9 @@ def test_a_workspace_whose_error_word_is_set_is_refused_by_the_kernel() -> None:
 
     launch()
     _nan_tiles_and_exact_elsewhere(out.cpu(), want)
-    assert ws[: 64 * 1024 - 4].view(torch.int32).eq(0).all()  # no counter was touched
+    assert int(ws[64 * 1024 - 4:64 * 1024].view(torch.int32).item()) == 2  # still refused until zeroed
+    launch()
+    _nan_tiles_and_exact_elsewhere(out.cpu(), want)
     ws.zero_()
     launch()
     assert torch.equal(out.cpu(), want)
