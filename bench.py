@@ -485,6 +485,23 @@ def main() -> int:
                                  "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
                 del g, blk, xp
             result[f"prefill_m{M}"] = prefill
+        # bf16 activations at M=512: the wide form after the per-row power-of-two
+        # conversion to fp16 (exact), fp32 sums rounded once to bf16
+        M = PREFILL_BATCHES[0]
+        prefill = {}
+        for name, K, N in C3_SHAPES:
+            lay = PackedTensorLayout.for_tensor(N, K)
+            blk = pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 3), layout=lay)
+            xp = synthetic.device_activations(M, K, seed=synthetic.SEED_BASE + 3, sigma=0.5).to(torch.bfloat16)
+            g = graph_of(lambda: [tq1_gemm_words(blk, xp, layout=lay, config=GemmConfig()) for _ in range(20)])
+            ms = time_graph(g) / 20
+            tflops = 2 * M * K * N / (ms * 1e-3) / 1e12
+            fp16_ms = result[f"prefill_m{M}"][name]["ms"]
+            prefill[name] = {"ms": round(ms, 4), "TFLOP/s": round(tflops, 2),
+                             "frac_of_mfma_f16_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                             "vs_fp16": round(ms / fp16_ms, 3)}
+            del g, blk, xp
+        result[f"prefill_m{M}_bf16"] = prefill
 
     # ---- the tied output head at M=1 (scope row f3): the largest GEMV of a token --
     if not args.no_model_stream:

@@ -33,8 +33,8 @@
  * undefined.
  *
  * Activations x are [M][columns] row-major, outputs y are [M][rows] row-major,
- * both of `dtype` (TERNEL_TQ1_F16 is the graded type; BF16/F32 also accepted by
- * the LUT path), fp32 accumulation throughout.
+ * both of `dtype` (TERNEL_TQ1_F16 is the graded type; BF16 also runs the wide
+ * MFMA form, F32 the LUT path only), fp32 accumulation throughout.
  *
  * Workspaces: a split workspace starts with a fixed 64 KiB region of
  * arrival counters whose last 32-bit word is the workspace's error word,
@@ -178,8 +178,8 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
                               int64_t columns, int dtype, int batch_tile, int k_split, void *stream);
 
 /*
- * MFMA product y = x @ W^T, fp16 activations, v_mfma_f32_32x32x16_f16 with fp32
- * accumulation, in one of three forms (the reference's GemmConfig forms,
+ * MFMA product y = x @ W^T, fp16 or bf16 activations, v_mfma_f32_32x32x16_f16
+ * with fp32 accumulation, in one of three forms (the reference's GemmConfig forms,
  * src/ternel_mlx/kernels.py:1043-1188, re-chosen for CDNA4):
  *   TERNEL_TQ1_GEMM_TILE   (prefill) 128x128 output tiles, weights decoded to
  *                          fp16 (t-1)*scale tiles in LDS;
@@ -198,6 +198,12 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
  *                          above, WIDE when it has at least CUs/4 output
  *                          tiles or 15 (tile, group) steps per CU, TILE
  *                          otherwise (and for a fixed k_split > 1).
+ * bf16 activations (dtype TERNEL_TQ1_BF16) run the WIDE form only (form AUTO
+ * or WIDE, no fixed k_split; size the workspace with form WIDE): a pre-pass
+ * scales each row by a power of two into fp16's range and converts it (exact:
+ * bf16's 8-bit significand fits fp16's 11 bits; values more than 2^28 below
+ * the row's largest lose bits), and the fp32 sums are scaled back and rounded
+ * once to bf16; inf and NaN propagate as in the reference. F32 is refused.
  * Replaces tq1_gemm, src/ternel_mlx/kernels.py:1287-1357. x is 16-byte
  * aligned in every form. k_split divides columns/128 (0 = auto). ws: ternel_tq1_gemm_workspace_bytes(...) bytes, the
  * same 64 KiB counter region + fp32 partials contract as ternel_tq1_matmul.
@@ -233,7 +239,8 @@ int ternel_tq1_get_rows_canonical(const uint8_t *blocks, int64_t rows, int64_t c
 
 /*
  * packed_matmul dispatch (src/ternel_mlx/modules.py:425-457): the LUT23 path
- * or an MFMA form and its split, from (M, rows, columns, dtype). ws sized by
+ * or an MFMA form and its split, from (M, rows, columns, dtype): fp32 always
+ * the LUT23 path, bf16 above the LUT23 batches the WIDE form. ws sized by
  * ternel_tq1_linear_workspace_bytes, same contract as ternel_tq1_matmul's.
  */
 int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows,
@@ -260,8 +267,8 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
  * (its MLP runs gate_proj, up_proj and the activation as separate mlx ops,
  * src/ternel_mlx/packed_model.py:72-92). Batches that ternel_tq1_linear sends
  * to the LUT23 kernel (up to 3 rows, 4 for matrices under 16 MiB, and every
- * bf16/fp32 batch) run it with the pair exchange in its epilogue; larger fp16
- * batches run the GEMM into the workspace and one elementwise pass. Workspace
+ * fp32 batch) run it with the pair exchange in its epilogue; larger fp16 and
+ * bf16 batches run the GEMM into the workspace and one elementwise pass. Workspace
  * from ternel_tq1_swiglu_workspace_bytes, same contract as ternel_tq1_linear's.
  */
 int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M, int64_t rows, int64_t columns,

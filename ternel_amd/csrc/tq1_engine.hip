@@ -1992,6 +1992,56 @@ __global__ __launch_bounds__(kThreads) void permute_activations_kernel(const uin
     }
 }
 
+// bf16 activations for the wide form: one workgroup per activation row. The
+// row's largest finite magnitude sets a power of two s that puts it in
+// [2^14, 2^15); the copy holds fp16(x s), in the wide form's K order when
+// PERMUTE (the permuted copy above), and inv[m] = 1 / s. The conversion is
+// exact: bf16's 8-bit significand fits fp16's 11 bits wherever x s is in
+// fp16's normal range, and only values more than 2^28 below the row's largest
+// lose bits (below 2^-38 of it they become zero). inf and NaN stay inf and
+// NaN. The wide kernel multiplies its fp32 sums by inv[m] (exact) and rounds
+// once to bf16.
+template <bool PERMUTE>
+__global__ __launch_bounds__(kThreads) void scale_rows_kernel(const uint16_t *__restrict__ x, _Float16 *__restrict__ xp,
+                                                             float *__restrict__ inv, int64_t K) {
+    __shared__ float wave_max[kThreads / 64];
+    const int64_t m = blockIdx.x;
+    const uint16_t *row = x + m * K;
+    _Float16 *out = xp + m * K;
+    float big = 0.0f;
+    for (int64_t k = threadIdx.x; k < K; k += kThreads) {
+        const float v = __uint_as_float(static_cast<uint32_t>(row[k]) << 16);
+        if (__builtin_isfinite(v)) big = fmaxf(big, fabsf(v));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off, 64));
+    if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = big;
+    __syncthreads();
+    big = wave_max[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) big = fmaxf(big, wave_max[w]);
+    int e = 0;
+    if (big > 0.0f) {
+        int exponent;
+        frexpf(big, &exponent);  // big = f 2^exponent, f in [0.5, 1)
+        e = min(14 - (exponent - 1), 126);
+    }
+    const float s = ldexpf(1.0f, e);
+    if (threadIdx.x == 0) inv[m] = ldexpf(1.0f, -e);
+    // 4-half units: unit u of the copy is unit direct_source_unit(u) of x
+    // (PERMUTE) or unit u.
+    for (int64_t unit = threadIdx.x; unit < K / 4; unit += kThreads) {
+        const int64_t group = unit >> 5;
+        const int u = static_cast<int>(unit & 31);
+        const int64_t src = group * 32 + (PERMUTE ? direct_source_unit(u) : u);
+        _Float16 h[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            h[j] = static_cast<_Float16>(__uint_as_float(static_cast<uint32_t>(row[src * 4 + j]) << 16) * s);
+        *reinterpret_cast<uint2 *>(out + unit * 4) = __builtin_bit_cast(uint2, h);
+    }
+}
+
 // Uses every decoded dword in an empty asm statement, so the decode of a
 // group stays in the step that computes it (else it is sunk past the step's
 // barrier toward the next step's MFMAs).
@@ -2016,10 +2066,13 @@ __device__ __forceinline__ void buffer_dma4(__amdgpu_buffer_rsrc_t rsrc, void *l
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void *)lds, 4, voffset, soffset, 0, 0);
 }
 
-template <int NB>
+// BF: the activations were bf16 (scale_rows_kernel): each output value is
+// the fp32 sum times its activation row's inv, rounded once to bf16.
+template <int NB, bool BF>
 __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
-    const uint32_t *__restrict__ packed, const _Float16 *__restrict__ xp, _Float16 *__restrict__ y,
-    float *__restrict__ partial, unsigned *__restrict__ counters, WideGeometry geo) {
+    const uint32_t *__restrict__ packed, const _Float16 *__restrict__ xp, uint16_t *__restrict__ y,
+    float *__restrict__ partial, unsigned *__restrict__ counters, const float *__restrict__ row_inv,
+    WideGeometry geo) {
     constexpr int kCols = NB * 32;                  // activation rows per tile
     constexpr int kXBytes = wide_x_bytes(NB);
     constexpr int kRing = wide_ring(NB);
@@ -2294,14 +2347,22 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
     // j + 32 swap half their values (as fp16 pairs) so that each holds two
     // runs of 8 consecutive rows: two 16-byte stores per lane, not 16 scattered
     // 2-byte ones. Every lane takes part in the swap; stores are guarded.
+    auto out_bits = [&](float v) -> uint32_t {
+        if constexpr (BF)
+            return from_f32<bf16_t>(v).bits;
+        else
+            return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    };
     auto store_frag = [&](int t, int nb, const float *vals) {
+        const int m = (t / geo.tiles_n) * kCols + nb * 32 + (lane & 31);
+        float sc = 1.0f;
+        if constexpr (BF) sc = row_inv[min(m, geo.M - 1)];
         uint32_t h[4][2];
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq)
 #pragma unroll
             for (int k = 0; k < 2; ++k)
-                h[qq][k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(vals[4 * qq + 2 * k]))) |
-                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(vals[4 * qq + 2 * k + 1]))) << 16);
+                h[qq][k] = out_bits(vals[4 * qq + 2 * k] * sc) | (out_bits(vals[4 * qq + 2 * k + 1] * sc) << 16);
         // rows 8qq + 4(lane / 32) + e; the lower lane keeps runs qq = 0, 2, the upper qq = 1, 3
         uint32_t r[4];
 #pragma unroll
@@ -2309,9 +2370,8 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
             const uint32_t send = upper ? h[(k >> 1) * 2][k & 1] : h[(k >> 1) * 2 + 1][k & 1];
             r[k] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, static_cast<int>(send)));
         }
-        const int m = (t / geo.tiles_n) * kCols + nb * 32 + (lane & 31);
         if (m >= geo.M) return;
-        _Float16 *yrow = y + static_cast<int64_t>(m) * geo.N;
+        uint16_t *yrow = y + static_cast<int64_t>(m) * geo.N;
 #pragma unroll
         for (int run = 0; run < 2; ++run) {  // rows 16 run + 8 (lane / 32) .. + 8
             const int n = (t % geo.tiles_n) * kWideRows + wave * 32 + 16 * run + (upper ? 8 : 0);
@@ -2325,19 +2385,18 @@ __global__ __launch_bounds__(kWideThreads) void wide_gemm_kernel(
                 const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    if (n + e < geo.N)
-                        yrow[n + e] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(d[e >> 1] >> (16 * (e & 1))));
+                    if (n + e < geo.N) yrow[n + e] = static_cast<uint16_t>(d[e >> 1] >> (16 * (e & 1)));
             }
         }
     };
-    // Tile t as fp16 NaN (0x7e00), the rows store_frag writes.
+    // Tile t as NaN (fp16 0x7e00, bf16 0x7fc0), the rows store_frag writes.
     auto store_nan_tile = [&](int t) {
-        const _Float16 nan16 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(0x7e00));
+        const uint16_t nan16 = BF ? 0x7fc0 : 0x7e00;
 #pragma unroll 1
         for (int nb = 0; nb < NB; ++nb) {
             const int m = (t / geo.tiles_n) * kCols + nb * 32 + (lane & 31);
             if (m >= geo.M) continue;
-            _Float16 *yrow = y + static_cast<int64_t>(m) * geo.N;
+            uint16_t *yrow = y + static_cast<int64_t>(m) * geo.N;
 #pragma unroll 1
             for (int run = 0; run < 2; ++run) {
                 const int n = (t % geo.tiles_n) * kWideRows + wave * 32 + 16 * run + (upper ? 8 : 0);
@@ -3137,30 +3196,62 @@ int plan_wide(int64_t M, int64_t rows, int64_t columns, int k_split, WidePlan *p
     plan->workgroups = static_cast<int>(wgs);
     // two partial slots per workgroup, each all of its waves' accumulators
     plan->partial_bytes = static_cast<size_t>(wgs) * 2 * kWideWaves * wide_frag_floats(plan->nb) * sizeof(float);
-    // the permuted copy of the activations follows the partials (four or
-    // eight blocks; one or two read x itself)
-    plan->xp_bytes = plan->nb <= 2 ? 0 : static_cast<size_t>(M) * columns * sizeof(_Float16);
+    // the fp16 copy of the activations follows the partials (permuted for four
+    // or eight blocks; one or two blocks read fp16 x itself and use the copy
+    // for bf16 only), then bf16 rows' inverse scales
+    plan->xp_bytes = static_cast<size_t>(M) * columns * sizeof(_Float16) + (M * sizeof(float) + 255) / 256 * 256;
     return TERNEL_TQ1_OK;
 }
 
-template <int NB>
+template <int NB, bool BF>
 int launch_wide_kernel(const uint32_t *packed, const _Float16 *xp, void *y, float *partial, unsigned *counters,
-                       const WideGeometry &geo, int workgroups, hipStream_t stream) {
-    int rc = ensure_lds_attribute(reinterpret_cast<const void *>(&wide_gemm_kernel<NB>),
+                       const float *row_inv, const WideGeometry &geo, int workgroups, hipStream_t stream) {
+    int rc = ensure_lds_attribute(reinterpret_cast<const void *>(&wide_gemm_kernel<NB, BF>),
                                   static_cast<int>(wide_lds_bytes(NB)));
     if (rc != TERNEL_TQ1_OK) return rc;
-    hipLaunchKernelGGL(wide_gemm_kernel<NB>, dim3(static_cast<unsigned>(workgroups)), dim3(kWideThreads),
-                       wide_lds_bytes(NB), stream, packed, xp, static_cast<_Float16 *>(y), partial, counters, geo);
+    hipLaunchKernelGGL((wide_gemm_kernel<NB, BF>), dim3(static_cast<unsigned>(workgroups)), dim3(kWideThreads),
+                       wide_lds_bytes(NB), stream, packed, xp, static_cast<uint16_t *>(y), partial, counters, row_inv,
+                       geo);
     TQ1_LAUNCH_CHECK();
     return TERNEL_TQ1_OK;
 }
 
-int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &plan, void *ws, hipStream_t stream) {
+template <bool BF>
+int launch_wide_nb(const uint32_t *packed, const _Float16 *xp, void *y, float *partial, unsigned *counters,
+                   const float *row_inv, const WidePlan &plan, const WideGeometry &geo, hipStream_t stream) {
+    switch (plan.nb) {
+        case 1:
+            return launch_wide_kernel<1, BF>(packed, xp, y, partial, counters, row_inv, geo, plan.workgroups, stream);
+        case 2:
+            return launch_wide_kernel<2, BF>(packed, xp, y, partial, counters, row_inv, geo, plan.workgroups, stream);
+        case 4:
+            return launch_wide_kernel<4, BF>(packed, xp, y, partial, counters, row_inv, geo, plan.workgroups, stream);
+        default:
+            return launch_wide_kernel<8, BF>(packed, xp, y, partial, counters, row_inv, geo, plan.workgroups, stream);
+    }
+}
+
+int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &plan, void *ws, hipStream_t stream,
+                int dtype) {
     unsigned *counters = static_cast<unsigned *>(ws);
     float *partial = reinterpret_cast<float *>(static_cast<char *>(ws) + kPartialOffset);
+    _Float16 *copy = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kPartialOffset + plan.partial_bytes);
+    WideGeometry geo = plan.geo;
+    geo.vector_rows = geo.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    if (dtype == TERNEL_TQ1_BF16) {
+        float *row_inv = reinterpret_cast<float *>(copy + static_cast<int64_t>(geo.M) * geo.G * kBlockWeights);
+        const int64_t K = static_cast<int64_t>(geo.G) * kBlockWeights;
+        if (plan.nb > 2)
+            hipLaunchKernelGGL(scale_rows_kernel<true>, dim3(static_cast<unsigned>(geo.M)), dim3(kThreads), 0, stream,
+                               static_cast<const uint16_t *>(x), copy, row_inv, K);
+        else
+            hipLaunchKernelGGL(scale_rows_kernel<false>, dim3(static_cast<unsigned>(geo.M)), dim3(kThreads), 0, stream,
+                               static_cast<const uint16_t *>(x), copy, row_inv, K);
+        TQ1_LAUNCH_CHECK();
+        return launch_wide_nb<true>(packed, copy, y, partial, counters, row_inv, plan, geo, stream);
+    }
     const _Float16 *xp = static_cast<const _Float16 *>(x);
     if (plan.nb > 2) {
-        _Float16 *copy = reinterpret_cast<_Float16 *>(static_cast<char *>(ws) + kPartialOffset + plan.partial_bytes);
         const int64_t quads = static_cast<int64_t>(plan.geo.M) * plan.geo.G * 8;  // 32-byte runs of the copy
         hipLaunchKernelGGL(permute_activations_kernel, dim3(static_cast<unsigned>(ceil_div(quads, kThreads))),
                            dim3(kThreads), 0, stream, static_cast<const uint2 *>(x), reinterpret_cast<uint2 *>(copy),
@@ -3168,18 +3259,7 @@ int launch_wide(const uint32_t *packed, const void *x, void *y, const WidePlan &
         TQ1_LAUNCH_CHECK();
         xp = copy;
     }
-    WideGeometry geo = plan.geo;
-    geo.vector_rows = geo.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
-    switch (plan.nb) {
-        case 1:
-            return launch_wide_kernel<1>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
-        case 2:
-            return launch_wide_kernel<2>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
-        case 4:
-            return launch_wide_kernel<4>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
-        default:
-            return launch_wide_kernel<8>(packed, xp, y, partial, counters, geo, plan.workgroups, stream);
-    }
+    return launch_wide_nb<false>(packed, xp, y, partial, counters, nullptr, plan, geo, stream);
 }
 
 // Automatic choice, from a sweep of every form over the 27B linears on MI355X
@@ -3230,10 +3310,19 @@ int resolve_gemm_form(int64_t M, int64_t rows, int64_t columns, int form, int k_
 constexpr int64_t kLinearLutMaxBatch = 3;
 constexpr int64_t kLinearLutMaxBatchSmall = 4;
 constexpr int64_t kLinearSmallMatrixBytes = 16ll << 20;
+// bf16 activations above the same batch run the wide form (scale_rows_kernel
+// then wide_gemm_kernel<NB, true>); fp32 ones always run the LUT23 kernel:
+// their 24-bit significands do not fit the matrix cores' fp16 operands.
 bool linear_uses_lut(int64_t M, int64_t rows, int64_t columns, int dtype) {
-    if (dtype != TERNEL_TQ1_F16) return true;
+    if (dtype == TERNEL_TQ1_F32) return true;
     const int64_t bytes = rows * (columns / kBlockWeights) * kBlockBytes;
     return M <= (bytes < kLinearSmallMatrixBytes ? kLinearLutMaxBatchSmall : kLinearLutMaxBatch);
+}
+
+// The GEMM form of the library's dispatch for a batch that does not take the
+// LUT23 kernel: bf16 activations run the wide form.
+int linear_gemm_form(int64_t M, int64_t rows, int64_t columns, int dtype) {
+    return dtype == TERNEL_TQ1_BF16 ? TERNEL_TQ1_GEMM_WIDE : TERNEL_TQ1_GEMM_AUTO;
 }
 
 int check_packed_pointer(const void *packed) {
@@ -3631,11 +3720,18 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
     g_last_error[0] = '\0';
     int rc;
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
-    if (dtype != TERNEL_TQ1_F16)
-        return fail(TERNEL_TQ1_EINVAL, "the MFMA path takes fp16 activations, got dtype code %d", dtype);
+    if (dtype != TERNEL_TQ1_F16 && dtype != TERNEL_TQ1_BF16)
+        return fail(TERNEL_TQ1_EINVAL, "the MFMA path takes fp16 or bf16 activations, got dtype code %d", dtype);
     if (form != TERNEL_TQ1_GEMM_AUTO && form != TERNEL_TQ1_GEMM_TILE && form != TERNEL_TQ1_GEMM_DIRECT &&
         form != TERNEL_TQ1_GEMM_WIDE)
         return fail(TERNEL_TQ1_EINVAL, "unknown GEMM form %d", form);
+    if (dtype == TERNEL_TQ1_BF16) {
+        if (form != TERNEL_TQ1_GEMM_AUTO && form != TERNEL_TQ1_GEMM_WIDE)
+            return fail(TERNEL_TQ1_EINVAL, "bf16 activations run the wide form (form %d or %d), got %d",
+                        TERNEL_TQ1_GEMM_AUTO, TERNEL_TQ1_GEMM_WIDE, form);
+        if (k_split > 1) return fail(TERNEL_TQ1_EINVAL, "the wide form takes no fixed K split, got %d", k_split);
+        form = TERNEL_TQ1_GEMM_WIDE;
+    }
     form = resolve_gemm_form(M, rows, columns, form, k_split);
     if (form == TERNEL_TQ1_GEMM_DIRECT) {
         DirectPlan direct;
@@ -3659,7 +3755,7 @@ int ternel_tq1_gemm(const uint32_t *packed, const void *x, void *y, int64_t M, i
         if (!ws || ws_bytes < need)
             return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
                         need);
-        return launch_wide(packed, x, y, wide, ws, static_cast<hipStream_t>(stream));
+        return launch_wide(packed, x, y, wide, ws, static_cast<hipStream_t>(stream), dtype);
     }
     GemmPlan plan;
     if ((rc = plan_gemm(M, rows, columns, k_split, &plan)) != TERNEL_TQ1_OK) return rc;
@@ -3694,21 +3790,22 @@ int ternel_tq1_get_rows_canonical(const uint8_t *blocks, int64_t rows, int64_t c
 size_t ternel_tq1_linear_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (linear_uses_lut(M, rows, columns, dtype))
         return ternel_tq1_matmul_workspace_bytes(M, rows, columns, 0, 0);
-    return ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
+    return ternel_tq1_gemm_workspace_bytes(M, rows, columns, linear_gemm_form(M, rows, columns, dtype), 0);
 }
 
 int ternel_tq1_linear(const uint32_t *packed, const void *x, void *y, int64_t M, int64_t rows, int64_t columns,
                       int dtype, void *ws, size_t ws_bytes, void *stream) {
     if (linear_uses_lut(M, rows, columns, dtype))
         return ternel_tq1_matmul(packed, x, y, M, rows, columns, dtype, 0, 0, ws, ws_bytes, stream);
-    return ternel_tq1_gemm(packed, x, y, M, rows, columns, dtype, TERNEL_TQ1_GEMM_AUTO, 0, ws, ws_bytes, stream);
+    return ternel_tq1_gemm(packed, x, y, M, rows, columns, dtype, linear_gemm_form(M, rows, columns, dtype), 0, ws,
+                           ws_bytes, stream);
 }
 
 // Where the GEMM path's fp16 gate/up output sits in the workspace: after the
 // GEMM's own workspace and never inside the counter region that every call
 // expects to find zero.
-static size_t swiglu_pairs_offset(int64_t M, int64_t rows, int64_t columns) {
-    const size_t gemm = ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
+static size_t swiglu_pairs_offset(int64_t M, int64_t rows, int64_t columns, int dtype) {
+    const size_t gemm = ternel_tq1_gemm_workspace_bytes(M, rows, columns, linear_gemm_form(M, rows, columns, dtype), 0);
     return (std::max(gemm, kPartialOffset) + 255) / 256 * 256;
 }
 
@@ -3718,14 +3815,14 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
     if (linear_uses_lut(M, rows, columns, dtype)) return TERNEL_TQ1_KERNEL_LUT23;
-    return resolve_gemm_form(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
+    return resolve_gemm_form(M, rows, columns, linear_gemm_form(M, rows, columns, dtype), 0);
 }
 
 size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK || rows % 2) return 0;
     if (linear_uses_lut(M, rows, columns, dtype))
         return ternel_tq1_matmul_workspace_bytes(M, rows, columns, uses_strip_gemv(M, 0, 0, rows, columns) ? 0 : 1, 0);
-    return swiglu_pairs_offset(M, rows, columns) + static_cast<size_t>(M) * rows * sizeof(_Float16);
+    return swiglu_pairs_offset(M, rows, columns, dtype) + static_cast<size_t>(M) * rows * sizeof(_Float16);
 }
 
 int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M, int64_t rows, int64_t columns,
@@ -3772,16 +3869,21 @@ int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M,
     if (need == 0 || !ws || ws_bytes < need)
         return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu a SwiGLU GEMM needs", ws_bytes,
                     need);
-    const size_t gemm = ternel_tq1_gemm_workspace_bytes(M, rows, columns, TERNEL_TQ1_GEMM_AUTO, 0);
-    void *pairs = static_cast<char *>(ws) + swiglu_pairs_offset(M, rows, columns);
-    if ((rc = ternel_tq1_gemm(packed, x, pairs, M, rows, columns, dtype, TERNEL_TQ1_GEMM_AUTO, 0, gemm ? ws : nullptr,
-                              gemm, stream)) != TERNEL_TQ1_OK)
+    const int gemm_form = linear_gemm_form(M, rows, columns, dtype);
+    const size_t gemm = ternel_tq1_gemm_workspace_bytes(M, rows, columns, gemm_form, 0);
+    void *pairs = static_cast<char *>(ws) + swiglu_pairs_offset(M, rows, columns, dtype);
+    if ((rc = ternel_tq1_gemm(packed, x, pairs, M, rows, columns, dtype, gemm_form, 0, gemm ? ws : nullptr, gemm,
+                              stream)) != TERNEL_TQ1_OK)
         return rc;
     const int64_t count = M * (rows / 2);
     int64_t grid = ceil_div(count, kThreads);
     if (grid > 65536) grid = 65536;
-    hipLaunchKernelGGL((swiglu_pairs_kernel<_Float16>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
-                       static_cast<const _Float16 *>(pairs), static_cast<_Float16 *>(z), count);
+    if (dtype == TERNEL_TQ1_BF16)
+        hipLaunchKernelGGL((swiglu_pairs_kernel<bf16_t>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
+                           static_cast<const bf16_t *>(pairs), static_cast<bf16_t *>(z), count);
+    else
+        hipLaunchKernelGGL((swiglu_pairs_kernel<_Float16>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
+                           static_cast<const _Float16 *>(pairs), static_cast<_Float16 *>(z), count);
     TQ1_LAUNCH_CHECK();
     return TERNEL_TQ1_OK;
 }

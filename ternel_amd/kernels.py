@@ -379,10 +379,13 @@ def tq1_gemm_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTenso
                    config: GemmConfig | None = None) -> torch.Tensor:
     """``x @ W.T`` on the MFMA kernels (reference tq1_gemm, kernels.py:1287-1357).
 
-    The matrix cores take fp16 activations (the graded type; weights are exact
-    in fp16). bf16 and fp32 activations -- whose range or precision fp16 would
-    not hold -- run through the LUT23 kernel, which computes in fp32 from the
-    activations as given, in as many launches as its counters need."""
+    The matrix cores take fp16 operands (weights are exact in fp16). fp16
+    activations run the form ``config`` names; bf16 ones run the wide form,
+    each row scaled by a power of two into fp16's range (exact: bf16's
+    significand fits fp16's) and the fp32 sums scaled back and rounded once to
+    bf16. fp32 activations -- whose significand fp16 would not hold -- and bf16
+    ones with a fixed K split run through the LUT23 kernel, which computes in
+    fp32 from the activations as given."""
     config = config or GemmConfig()
     check_packed(packed, layout=layout)
     batch = check_activations(x, layout=layout)
@@ -390,9 +393,14 @@ def tq1_gemm_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTenso
         raise FormatError(
             f"k split {config.k_split} does not divide the tensor's {layout.groups_per_row} groups per row"
         )
-    if x.dtype != torch.float16:
+    if x.dtype == torch.float32 or (x.dtype == torch.bfloat16 and config.k_split > 1):
         return tq1_matmul_words(packed, x, layout=layout, config=MatmulConfig(batch_tile=1, k_split=config.k_split))
-    form_name = config.form_for(batch)
+    if x.dtype == torch.bfloat16:
+        if config.form not in ("auto", "wide"):
+            raise FormatError(f"bf16 activations run the wide GEMM form, not {config.form!r}")
+        form_name = "wide"
+    else:
+        form_name = config.form_for(batch)
     if form_name == "direct" and batch > DIRECT_MAX_BATCH:
         raise FormatError(f"the direct-fragment form takes at most {DIRECT_MAX_BATCH} activation rows, got {batch}")
     form = GEMM_FORMS[form_name]
@@ -404,7 +412,7 @@ def tq1_gemm_words(packed: torch.Tensor, x: torch.Tensor, *, layout: PackedTenso
     ws = workspace(x.device, need)
     _lib.check(handle.ternel_tq1_gemm(
         packed.data_ptr(), x.data_ptr(), out.data_ptr(), batch, layout.rows, layout.columns,
-        _lib.DTYPE_F16, form, config.k_split, ws.data_ptr() if ws is not None else None,
+        _DTYPE_CODE[x.dtype], form, config.k_split, ws.data_ptr() if ws is not None else None,
         ws.numel() if ws is not None else 0, _stream(x.device)))
     _watch(ws, form_name == "wide" or (form_name == "auto" and batch > WIDE_MIN_AUTO_BATCH))
     return out

@@ -37,9 +37,13 @@ def test_the_module_dispatch_follows_the_library() -> None:
         assert select_kernel(layout, row["M"], torch.float16) == ("lut23" if code == 100 else "gemm")
 
 
-def test_non_fp16_activations_always_take_the_lut_kernel() -> None:
-    for dtype in (_lib.DTYPE_BF16, _lib.DTYPE_F32):
-        assert _lib.lib().ternel_tq1_linear_kernel(512, 17408, 5120, dtype) == 100
+def test_fp32_activations_take_the_lut_kernel_and_bf16_the_wide_form() -> None:
+    handle = _lib.lib()
+    for M in (1, 3, 8, 64, 512, 2048):
+        assert handle.ternel_tq1_linear_kernel(M, 17408, 5120, _lib.DTYPE_F32) == 100
+        # bf16: the LUT23 kernel where fp16 takes it, the wide form (3) above
+        fp16 = handle.ternel_tq1_linear_kernel(M, 17408, 5120, _lib.DTYPE_F16)
+        assert handle.ternel_tq1_linear_kernel(M, 17408, 5120, _lib.DTYPE_BF16) == (100 if fp16 == 100 else 3)
 
 
 def test_the_sweep_covers_every_regime() -> None:

@@ -269,7 +269,9 @@ def test_workspace_queries() -> None:
     assert handle.ternel_tq1_gemm_workspace_bytes(65, 256, 5120, direct, 1) == 0  # rejected
     # wide form: two fp32 partial slots of 8 waves x NB fragments x 16 x 64 per
     # workgroup (one per CU, 256 without a GPU, at most one per unit), then
-    # the K-permuted fp16 copy of the activations (four or eight blocks only);
+    # the fp16 copy of the activations (K-permuted at four or eight blocks;
+    # fp16 x is read in place at one or two, bf16 x always converted into it),
+    # then the bf16 rows' inverse scales (M floats, in 256-byte units);
     # NB = 1, 2, 4, 8 32-row activation blocks per tile for M <= 32, 64, 128, above,
     # and 4 instead of 8 while, with 256-wide tiles, the partials a tile's last
     # contributor reads (256/tiles - 1) exceed a tenth of the steps per CU
@@ -277,22 +279,28 @@ def test_workspace_queries() -> None:
     wide = 3
     def slot_pair(nb: int) -> int:
         return 2 * 8 * nb * 16 * 64 * 4
+
+    def copy(M: int, K: int) -> int:
+        return M * K * 2 + (M * 4 + 255) // 256 * 256
     # gate/up, 68 x 2 tiles, 40 groups: 0.9 partials after 21.25 steps
     assert handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, wide, 0) == (
-        counters + 256 * slot_pair(8) + 512 * 5120 * 2)
+        counters + 256 * slot_pair(8) + copy(512, 5120))
     # gate/up, 68 tiles: 2.8 partials after 10.6 steps
     assert handle.ternel_tq1_gemm_workspace_bytes(256, 17408, 5120, wide, 0) == (
-        counters + 256 * slot_pair(4) + 256 * 5120 * 2)
+        counters + 256 * slot_pair(4) + copy(256, 5120))
     # down, 20 x 4 tiles, 136 groups: 2.2 partials after 42.5 steps; 20 x 3: 3.3 after 31.9
     assert handle.ternel_tq1_gemm_workspace_bytes(1024, 5120, 17408, wide, 0) == (
-        counters + 256 * slot_pair(8) + 1024 * 17408 * 2)
+        counters + 256 * slot_pair(8) + copy(1024, 17408))
     assert handle.ternel_tq1_gemm_workspace_bytes(768, 5120, 17408, wide, 0) == (
-        counters + 256 * slot_pair(4) + 768 * 17408 * 2)
-    # one or two blocks read x itself: no permuted copy
-    assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 1) == counters + 5 * slot_pair(1)
-    assert handle.ternel_tq1_gemm_workspace_bytes(64, 17408, 5120, wide, 0) == counters + 256 * slot_pair(2)
+        counters + 256 * slot_pair(4) + copy(768, 17408))
+    assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 1) == counters + 5 * slot_pair(1) + copy(5, 640)
+    assert handle.ternel_tq1_gemm_workspace_bytes(64, 17408, 5120, wide, 0) == (
+        counters + 256 * slot_pair(2) + copy(64, 5120))
     assert handle.ternel_tq1_gemm_workspace_bytes(100, 17408, 5120, wide, 0) == (
-        counters + 256 * slot_pair(4) + 100 * 5120 * 2)
+        counters + 256 * slot_pair(4) + copy(100, 5120))
+    # bf16 through the library's dispatch: the wide form's workspace
+    assert handle.ternel_tq1_linear_workspace_bytes(512, 17408, 5120, 1) == (
+        handle.ternel_tq1_gemm_workspace_bytes(512, 17408, 5120, wide, 0))
     assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 640, wide, 2) == 0  # K is split by stream-K
     assert handle.ternel_tq1_gemm_workspace_bytes(5, 256, 1 << 22, wide, 0) == 0  # 32-bit buffer offsets
     assert handle.ternel_tq1_packed_words(300, 640) == 5 * 5 * 7 * 64
