@@ -534,6 +534,8 @@ def main() -> int:
 
 PHASES = ("start", "activations arrived", "first words issued", "own tables written", "tables ready (barrier)",
           "blocks summed", "partial stored and acknowledged", "arrival counted", "fix-up done")
+# The strip GEMV's stamps (M=1 where a CU's share of the rows is below 64: QKV).
+STRIP_PHASES = ("start", "activations arrived, first words issued", "tables ready", "all items summed", "done")
 # The wide form's stamps in the same slots (2-4 unused; 7 and 8 only where it reduces a shared tile).
 WIDE_PHASES = ("start", "first unit's operands in LDS", "-", "-", "-", "segment summed", "arrival counted",
                "other contributors' partials published", "tile stored")
@@ -571,7 +573,9 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
 
     for i, (name, K, N) in enumerate(C1_SHAPES):
         wide = batch > 1 and handle.ternel_tq1_linear_kernel(batch, N, K, 0) == 3  # TERNEL_TQ1_GEMM_WIDE
-        names = WIDE_PHASES if wide else PHASES
+        strip = batch == 1 and handle.ternel_tq1_matmul_workspace_bytes(1, N, K, 0, 0) == 0  # needs no workspace
+        lut = handle.ternel_tq1_linear_kernel(batch, N, K, 0) == 100  # TERNEL_TQ1_KERNEL_LUT23
+        names = WIDE_PHASES if wide else (STRIP_PHASES if strip else PHASES)
         lay = PackedTensorLayout.for_tensor(N, K)
         ring = ring_copies(packed_bytes(K, N))
         weights = [pack_weights(synthetic.device_blocks(N, K, seed=synthetic.SEED_BASE + 1 + 100 * r + i), layout=lay)
@@ -599,7 +603,7 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
                         phase_times[phase] += [(st[p] - t0) / 100 for st in mine if st[p]]
                 ranked = sorted(mine, key=lambda st: st[0])
                 quarter = max(1, len(ranked) // 4)
-                for q in range(4):
+                for q in range(4 if names is PHASES else 0):
                     part = ranked[q * quarter:(q + 1) * quarter] if q < 3 else ranked[3 * quarter:]
                     by_start[q] += [((st[0] - t0) / 100, (st[3] - st[0]) / 100, (st[1] - st[0]) / 100,
                                      (st[2] - st[1]) / 100) for st in part if st[3] and st[1] and st[2]]
@@ -616,6 +620,8 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
             continue
         print(json.dumps({
             "phase_profile": name, "K": K, "N": N, "M": batch, "waves_per_launch": len(phase_times["start"]) // 3,
+            "kernel": "wide_gemm_kernel" if wide else ("strip_gemv_kernel" if strip else
+                                                        ("lut_gemv_kernel" if lut else "direct_gemm_kernel")),
             "gemv_graph_us": round(graph_ms * 1e3, 3),
             "xcc_span_us": quantiles(spans),
             "phases_after_xcc_first_wave_start": {ph: quantiles(v) for ph, v in phase_times.items() if v},
