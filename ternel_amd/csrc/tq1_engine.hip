@@ -649,6 +649,21 @@ __device__ __forceinline__ uint32_t lut_address_hi(uint32_t pair, uint32_t base)
     return r;
 }
 
+// a * b + c and a * b for a, b below 2^24 (v_mad_u32_u24 / v_mul_u32_u24).
+// Written out because the compiler turns a 32-bit multiply-add into a 64-bit
+// v_mad_u64_u32 whose unused high addend the register allocator may place in
+// a register with a load still in flight, and then waits for that load.
+__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ void split_pair(uint32_t pair, uint32_t base, uint32_t &lo_a, uint32_t &hi_a,
                                            uint32_t &lo_b, uint32_t &hi_b) {
     const u16x2 p = __builtin_bit_cast(u16x2, pair);
@@ -940,8 +955,9 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
 // they stay for the whole launch, so a lane may look up any group. The
 // strip's R x G blocks are numbered t = g R + i (row i, group g), so
 // consecutive lanes read consecutive rows of one group, and cut into items
-// of 64; the 16 waves take contiguous runs of items, each keeping the next
-// item's words in flight while it sums one. Every load is issued
+// of 64; wave w takes items w, w + 16, ..., with its first two items' words
+// requested before the tables are built and, after that, the words of the
+// item two ahead requested as it sums one. Every load is issued
 // unconditionally (past the end of a run a wave re-reads the item it sums,
 // from cache), so the compiler's wait counts stay exact: a wait for one item
 // never waits for the next.
@@ -957,6 +973,7 @@ constexpr int kStripWaves = 16;
 constexpr int kStripThreads = kStripWaves * 64;
 constexpr int kStripMaxGroups = 40;
 constexpr int kStripMaxRows = 62;
+constexpr int kStripSumWaves = (kStripMaxRows + 63) / 64;
 constexpr int kStripLdsFloats = 40960;  // 160 KiB, the workgroup limit
 static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows <= kStripLdsFloats, "LDS fits");
 constexpr int kStripTrit3Iters = (kStripMaxGroups * (kFullSlots + 1) + kStripThreads - 1) / kStripThreads;
@@ -1107,8 +1124,12 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     const int R = strip_row(s + 1, geo) - lo;
     const int RG = R * G;
     const int n_items = (RG + 63) >> 6;
-    const int i0 = (wave * n_items) >> 4;
-    const int i1 = ((wave + 1) * n_items) >> 4;
+    // Wave w sums items w, w + 16, w + 32, ...: the waves' shares differ by
+    // at most one item. Past its last item a wave's loads re-read the last
+    // item it owns (a wave that owns none, the strip's last item).
+    const int n_own = n_items > wave ? (n_items - wave + kStripWaves - 1) / kStripWaves : 0;
+    const int own_last = n_own > 0 ? wave + (n_own - 1) * kStripWaves : n_items - 1;
+    auto item_of = [&](int j) __attribute__((always_inline)) { return min(wave + j * kStripWaves, own_last); };
     const float inv_r = 1.0f / static_cast<float>(max(R, 1));
 
     // Block t = g R + i of item i for this lane (clamped into the strip):
@@ -1117,8 +1138,10 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
         t = (item << 6) + lane;
         const int tc = min(t, max(RG - 1, 0));
         g = static_cast<int>((static_cast<float>(tc) + 0.5f) * inv_r);
-        const int row = lo + (tc - g * R);
-        return ((row >> 6) * G + g) * kTileGroupWords + (row & 63);
+        // (Every factor and result here is below 2^24.)
+        const uint32_t row = static_cast<uint32_t>(lo + tc) - mul_u24(static_cast<uint32_t>(g), static_cast<uint32_t>(R));
+        return static_cast<int>(mad_u24(mad_u24(row >> 6, static_cast<uint32_t>(G), static_cast<uint32_t>(g)),
+                                        static_cast<uint32_t>(kTileGroupWords), row & 63u));
     };
     // (The scheduling barriers keep the sums of the item before from moving
     // above the loads, where they would wait for that item's words first.)
@@ -1131,9 +1154,11 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
         __builtin_amdgcn_sched_barrier(0);
     };
 
+    // The first two items' words are in flight while the tables are built.
     wait_vector_memory();
     uint32_t wa[kBlockWords], wb[kBlockWords];
-    load(min(i0, n_items - 1), wa);
+    load(item_of(0), wa);
+    load(item_of(1), wb);
     TQ1_PHASE(strip_wave_id, 1);  // activations arrived, first words issued
 
     if constexpr (STAGE) {
@@ -1150,29 +1175,31 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     auto consume = [&](int item, const uint32_t (&w)[kBlockWords]) __attribute__((always_inline)) {
         int t, g;
         (void)block(item, t, g);
-        const float sum = strip_block_sum(w, lds, static_cast<uint32_t>(g * kLutFloats * 4));
+        const float sum = strip_block_sum(w, lds, mul_u24(static_cast<uint32_t>(g), kLutFloats * 4));
         if (t < RG) lds_f[geo.value_base + t] = half_bits_to_float(w[0]) * sum;
     };
     // No branch separates a load from the loop's other loads, so every path
-    // into the loop head carries the same seven loads in flight.
-    for (int k = i0; k < i1; k += 2) {
-        load(min(k + 1, i1 - 1), wb);
-        consume(k, wa);
-        load(min(k + 2, i1 - 1), wa);
-        if (k + 1 < i1) consume(k + 1, wb);
+    // into the loop head carries the same fourteen loads in flight (wa's
+    // issued before wb's).
+    for (int j = 0; j < n_own; j += 2) {
+        consume(item_of(j), wa);
+        load(item_of(j + 2), wa);
+        if (j + 1 < n_own) consume(item_of(j + 1), wb);
+        load(item_of(j + 3), wb);
     }
     TQ1_PHASE(strip_wave_id, 3);  // all items summed
     __syncthreads();
 
-    // Row i by lane i of wave 0: its G block values in group order.
-    if (wave == 0) {
+    // Row i by lane i % 64 of wave i / 64: its G block values in group order.
+    if (wave < kStripSumWaves) {
+        const int i = wave * 64 + lane;
         float total = 0.0f;
-        if (lane < R) {
-            const float *v = lds_f + geo.value_base + lane;
+        if (i < R) {
+            const float *v = lds_f + geo.value_base + i;
             total = v[0];
             for (int g = 1; g < G; ++g) total += v[g * R];
         }
-        strip_store<T, GLU>(y, lo + lane, lane, lane < R, total);
+        strip_store<T, GLU>(y, lo + i, lane, i < R, total);
     }
     TQ1_PHASE(strip_wave_id, 4);  // done
 }

@@ -42,9 +42,12 @@ def run(blocks: np.ndarray, x: torch.Tensor) -> torch.Tensor:
     return out
 
 
-# (rows, columns): QKV; 4096^2; one group; strips of 8 and 10 rows (2050 rows
-# over 256 CUs) and an odd last strip; the 62-row edge (15872 rows); 12 groups.
-SHAPES = ((8192, 5120), (4096, 4096), (2048, 128), (2050, 640), (3001, 1024), (15872, 5120), (6144, 1536))
+# (rows, columns): QKV (20 items of 64 blocks per strip: waves 0-3 sum two,
+# the rest one); 4096^2; one group; strips of 8 and 10 rows (2050 rows over 256
+# CUs) and an odd last strip; the 62-row edge (15872 rows); 12 groups; 16 items
+# per strip (one per wave).
+SHAPES = ((8192, 5120), (4096, 4096), (2048, 128), (2050, 640), (3001, 1024), (15872, 5120), (6144, 1536),
+          (8192, 4096))
 
 
 @pytest.mark.parametrize(("rows", "columns"), SHAPES)
