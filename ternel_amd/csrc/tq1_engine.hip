@@ -722,8 +722,10 @@ __device__ __forceinline__ T swiglu_pair(T gate, T up) {
     return from_f32<T>(g / (1.0f + expf(-g)) * to_f32<T>(up));
 }
 
-template <typename T, int C, int BT, bool GLU = false, int KW = 1>
-__global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
+// RT 64-row tiles per workgroup (4, or 2 where 256-row blocks would leave
+// fewer than about 1.5 workgroups per CU).
+template <typename T, int C, int BT, bool GLU = false, int KW = 1, int RT = kThreads / kTileRows>
+__global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
     const uint32_t *__restrict__ packed, const T *__restrict__ x, T *__restrict__ y,
     float *__restrict__ partial, unsigned *__restrict__ counters, int M, int N, int G, int chunk_groups,
     int k_split) {
@@ -737,17 +739,19 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     // few resident per CU.)
     static_assert(KW == 1 || KW == 2, "one or two waves per row tile");
     static_assert(C % KW == 0, "each wave stream takes whole blocks");
-    constexpr int NT = kThreads * KW;
+    static_assert(RT == 2 || RT == 4, "128- or 256-row workgroups");
+    constexpr int RB = RT * kTileRows;  // rows per workgroup (threads per wave stream)
+    constexpr int NT = RB * KW;
     constexpr int CB = C / KW;
     __shared__ float lut[BT][C][kLutFloats];
     __shared__ __align__(16) T xs[BT][C * kBlockWeights];
-    __shared__ float2 xchg[KW > 1 ? (KW - 1) * CB * BT : 1][kThreads];
+    __shared__ float2 xchg[KW > 1 ? (KW - 1) * CB * BT : 1][RB];
     __shared__ unsigned s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int stream = __builtin_amdgcn_readfirstlane(tid / kThreads);  // wave-uniform, branched on as such
-    const int tile = blockIdx.x * (kThreads / kTileRows) + ((tid & (kThreads - 1)) >> 6);
+    const int stream = __builtin_amdgcn_readfirstlane(tid / RB);  // wave-uniform, branched on as such
+    const int tile = blockIdx.x * RT + ((tid & (RB - 1)) >> 6);
     const int row = tile * kTileRows + lane;
     const bool row_ok = row < N && stream == 0;  // lanes that hold and write the result
     const int b0 = blockIdx.y * BT;
@@ -759,7 +763,7 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
     const int load_tile = min(tile, (N + kTileRows - 1) / kTileRows - 1);
     const uint32_t *row_words = packed + static_cast<int64_t>(load_tile) * G * kTileGroupWords + lane;
     const int lut_wave_id =
-        ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * KW * (kThreads / 64) + (tid >> 6);
+        ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * KW * RT + (tid >> 6);
     (void)lut_wave_id;
     TQ1_PHASE(lut_wave_id, 0);  // wave start
     TQ1_PHASE_XCC(lut_wave_id);
@@ -842,7 +846,7 @@ __global__ __launch_bounds__(kThreads * KW) void lut_gemv_kernel(
                 if (KW == 1 || stream == 0)
                     acc[j] = fmaf(scale, sum[j], acc[j]);
                 else
-                    xchg[((stream - 1) * CB + c) * BT + j][tid & (kThreads - 1)] = make_float2(sum[j], scale);
+                    xchg[((stream - 1) * CB + c) * BT + j][tid & (RB - 1)] = make_float2(sum[j], scale);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -2741,6 +2745,7 @@ constexpr size_t kPartialOffset = kCounterRegionBytes;
 struct LutPlan {
     int batch_tile;
     int waves;         // waves per 64-row tile (compile-time KW)
+    int row_tiles;     // 64-row tiles per workgroup (compile-time RT)
     int chunk;         // groups per sub-chunk (compile-time C)
     int chunk_groups;  // groups per workgroup, a multiple of chunk
     int k_split;
@@ -2771,6 +2776,7 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
         return fail(TERNEL_TQ1_EINVAL, "batch tile must be 1, 2 or 4, got %d", batch_tile);
     plan->batch_tile = batch_tile;
     plan->waves = 1;
+    plan->row_tiles = kThreads / kTileRows;
     plan->row_blocks = ceil_div(rows, kThreads);
     plan->batch_tiles = ceil_div(M, batch_tile);
     if (k_split < 0) return fail(TERNEL_TQ1_EINVAL, "k split must be positive, got %d", k_split);
@@ -2819,6 +2825,17 @@ int plan_lut(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_spl
     if (plan->batch_tile == 1 && plan->chunk >= 2 &&
         (plan->chunk >= 8 || plan->row_blocks * plan->batch_tiles * plan->k_split <= 3 * device_cu_count()))
         plan->waves = 2;
+    // One vector over a split whose 256-row workgroups number fewer than 1.5
+    // per CU (the 340 of down 17408->5120 leave a third of the CUs running two
+    // and the rest one): 128-row workgroups, twice as many, even the CUs out.
+    // Measured on MI355X (graph-replayed, cold, us, 256 -> 128 rows): down
+    // 10.64 -> 10.21, O 8192->5120 8.49 -> 8.27; gate/up (680 workgroups)
+    // 9.60 -> 9.74, so not there.
+    if (plan->batch_tile == 1 && plan->k_split > 1 &&
+        2 * plan->row_blocks * plan->batch_tiles * plan->k_split <= 3 * device_cu_count()) {
+        plan->row_tiles = 2;
+        plan->row_blocks = ceil_div(rows, plan->row_tiles * kTileRows);
+    }
     if (plan->k_split > 65535) return fail(TERNEL_TQ1_EINVAL, "K too large for one launch");
     // A split launch needs one arrival counter per (row block, batch tile):
     // a batch past what the counter region holds runs as several launches
@@ -2863,17 +2880,30 @@ void launch_lut_kernel(const LutPlan &plan, const uint32_t *packed, const void *
                        unsigned *counters, int64_t M, int64_t rows, int G, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(plan.row_blocks), static_cast<unsigned>(plan.batch_tiles),
                     static_cast<unsigned>(plan.k_split));
-    if constexpr (BT == 1 && C >= 2) {
-        if (plan.waves == 2) {
-            hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU, 2>), grid, dim3(2 * kThreads), 0, stream, packed,
-                               static_cast<const T *>(x), static_cast<T *>(y), partial, counters,
-                               static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
+#define TQ1_LUT_KERNEL_LAUNCH(KW, RT)                                                                          \
+    hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU, KW, RT>), grid, dim3(KW * RT * kTileRows), 0, stream,     \
+                       packed, static_cast<const T *>(x), static_cast<T *>(y), partial, counters,                \
+                       static_cast<int>(M), static_cast<int>(rows), G, plan.chunk_groups, plan.k_split)
+    if constexpr (BT == 1) {
+        if (plan.row_tiles == 2) {
+            if constexpr (C >= 2) {
+                if (plan.waves == 2) {
+                    TQ1_LUT_KERNEL_LAUNCH(2, 2);
+                    return;
+                }
+            }
+            TQ1_LUT_KERNEL_LAUNCH(1, 2);
             return;
         }
     }
-    hipLaunchKernelGGL((lut_gemv_kernel<T, C, BT, GLU>), grid, dim3(kThreads), 0, stream, packed,
-                       static_cast<const T *>(x), static_cast<T *>(y), partial, counters, static_cast<int>(M),
-                       static_cast<int>(rows), G, plan.chunk_groups, plan.k_split);
+    if constexpr (BT == 1 && C >= 2) {
+        if (plan.waves == 2) {
+            TQ1_LUT_KERNEL_LAUNCH(2, 4);
+            return;
+        }
+    }
+    TQ1_LUT_KERNEL_LAUNCH(1, 4);
+#undef TQ1_LUT_KERNEL_LAUNCH
 }
 
 template <typename T>

@@ -271,3 +271,17 @@ def test_auto_split_gemv_carries_non_finite_activations_to_every_row(bad: float,
     want = O.oracle_matmul(blocks, x, rows=rows, columns=5120)
     assert int(np.count_nonzero(np.isfinite(got))) == 0
     assert O.compare(got, want)["pattern_mismatches"] == 0
+
+
+@pytest.mark.parametrize(("rows", "columns"), ((5120, 17408), (5120, 8192)))
+def test_a_vector_sums_the_same_in_any_batch_and_workgroup_shape(rows: int, columns: int) -> None:
+    """At M=1 these splits run 128-row workgroups (down: 340 of 256 rows would
+    leave most CUs one and some two), at M=2 256-row ones: each row's chunk
+    and block order is the same, so the first vector's outputs are identical."""
+    blocks = random_blocks(rows, columns, seed=rows + columns)
+    x = np.random.default_rng(columns).normal(0.0, 1.0, size=(2, columns)).astype(np.float32)
+    one = run_auto(blocks, x[:1]).cpu().numpy()
+    two = run_auto(blocks, x).cpu().numpy()
+    np.testing.assert_array_equal(two[:1], one)
+    oracle = O.oracle_matmul(blocks, x[:1], rows=rows, columns=columns)
+    assert O.compare(one, oracle)["normalised_max_abs_error"] < NORTH_STAR_TOLERANCE
