@@ -2039,10 +2039,27 @@ __global__ __launch_bounds__(kThreads) void scale_rows_kernel(const uint16_t *__
     const int64_t m = blockIdx.x;
     const uint16_t *row = x + m * K;
     _Float16 *out = xp + m * K;
+    // K is a multiple of 128, so rows of x and xp start 16-byte aligned
+    // whenever x and xp do: then 16-byte reads (8 values) and writes, else
+    // one value at a time.
+    const bool wide = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(xp)) & 15u) == 0;
+    auto finite_abs = [](uint32_t bits) {
+        const float v = __uint_as_float(bits);
+        return __builtin_isfinite(v) ? fabsf(v) : 0.0f;
+    };
     float big = 0.0f;
-    for (int64_t k = threadIdx.x; k < K; k += kThreads) {
-        const float v = __uint_as_float(static_cast<uint32_t>(row[k]) << 16);
-        if (__builtin_isfinite(v)) big = fmaxf(big, fabsf(v));
+    if (wide) {
+        const uint4 *r4 = reinterpret_cast<const uint4 *>(row);
+        for (int64_t c = threadIdx.x; c < K / 8; c += kThreads) {
+            const uint4 v = r4[c];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                big = fmaxf(big, fmaxf(finite_abs(w[i] << 16), finite_abs(w[i] & 0xffff0000u)));
+        }
+    } else {
+        for (int64_t k = threadIdx.x; k < K; k += kThreads)
+            big = fmaxf(big, finite_abs(static_cast<uint32_t>(row[k]) << 16));
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off, 64));
@@ -2061,15 +2078,31 @@ __global__ __launch_bounds__(kThreads) void scale_rows_kernel(const uint16_t *__
     if (threadIdx.x == 0) inv[m] = ldexpf(1.0f, -e);
     // 4-half units: unit u of the copy is unit direct_source_unit(u) of x
     // (PERMUTE) or unit u.
-    for (int64_t unit = threadIdx.x; unit < K / 4; unit += kThreads) {
-        const int64_t group = unit >> 5;
-        const int u = static_cast<int>(unit & 31);
-        const int64_t src = group * 32 + (PERMUTE ? direct_source_unit(u) : u);
-        _Float16 h[4];
+    auto scaled = [&](uint32_t bits) { return static_cast<_Float16>(__uint_as_float(bits) * s); };
+    auto pair = [&](uint32_t w) {  // two bf16 values -> two fp16 values, low first
+        const _Float16 h[2] = {scaled(w << 16), scaled(w & 0xffff0000u)};
+        return __builtin_bit_cast(uint32_t, h);
+    };
+    if (wide) {
+        const uint2 *r2 = reinterpret_cast<const uint2 *>(row);
+        uint4 *o4 = reinterpret_cast<uint4 *>(out);
+        for (int64_t c = threadIdx.x; c < K / 8; c += kThreads) {  // copy chunk c: units 2c, 2c + 1
+            const int64_t group = c >> 4;
+            const int u = static_cast<int>(c & 15) * 2;
+            const uint2 a = r2[group * 32 + (PERMUTE ? direct_source_unit(u) : u)];
+            const uint2 b = r2[group * 32 + (PERMUTE ? direct_source_unit(u + 1) : u + 1)];
+            o4[c] = uint4{pair(a.x), pair(a.y), pair(b.x), pair(b.y)};
+        }
+    } else {
+        for (int64_t unit = threadIdx.x; unit < K / 4; unit += kThreads) {
+            const int64_t group = unit >> 5;
+            const int u = static_cast<int>(unit & 31);
+            const int64_t src = group * 32 + (PERMUTE ? direct_source_unit(u) : u);
+            _Float16 h[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            h[j] = static_cast<_Float16>(__uint_as_float(static_cast<uint32_t>(row[src * 4 + j]) << 16) * s);
-        *reinterpret_cast<uint2 *>(out + unit * 4) = __builtin_bit_cast(uint2, h);
+            for (int j = 0; j < 4; ++j) h[j] = scaled(static_cast<uint32_t>(row[src * 4 + j]) << 16);
+            *reinterpret_cast<uint2 *>(out + unit * 4) = __builtin_bit_cast(uint2, h);
+        }
     }
 }
 

@@ -147,3 +147,23 @@ def test_bf16_takes_no_other_mfma_form() -> None:
                                 _lib.DTYPE_BF16, 2, 0, None, 0, None)
     assert rc == _lib.TERNEL_TQ1_EINVAL
     assert "bf16 activations run the wide form" in _lib.last_error()
+
+
+@pytest.mark.parametrize("batch", (64, 300))  # two blocks (x in its own order), eight (permuted copy)
+def test_unaligned_bf16_activations_give_the_same_result(batch) -> None:
+    """The row-scaling pass reads 16-byte chunks when x is 16-byte aligned and
+    single values otherwise: both give the same copy, so the same outputs."""
+    rows, columns = 1024, 2560
+    blocks = random_blocks(rows, columns, seed=43)
+    packed = pack(blocks)
+    x = to_dev(np.random.default_rng(43).normal(0.0, 1.0, size=(batch, columns)).astype(np.float32)).to(torch.bfloat16)
+    storage = torch.zeros(batch * columns + 8, dtype=torch.bfloat16, device=dev())
+    shifted = storage[1:1 + batch * columns].view(batch, columns)
+    shifted.copy_(x)
+    assert shifted.data_ptr() % 16 != 0 and x.data_ptr() % 16 == 0
+    lay = layout(rows, columns)
+    aligned = tq1_gemm_words(packed, x, layout=lay, config=GemmConfig(form="wide"))
+    unaligned = tq1_gemm_words(packed, shifted, layout=lay, config=GemmConfig(form="wide"))
+    assert torch.equal(aligned.view(torch.int16), unaligned.view(torch.int16))
+    want = O.oracle_matmul(blocks, bf16_host(x), rows=rows, columns=columns)
+    assert O.compare(aligned.float().cpu().numpy(), want)["normalised_max_abs_error"] < BF16_TOLERANCE
