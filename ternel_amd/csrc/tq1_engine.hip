@@ -959,9 +959,9 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // they stay for the whole launch, so a lane may look up any group. The
 // strip's R x G blocks are numbered t = g R + i (row i, group g), so
 // consecutive lanes read consecutive rows of one group, and cut into items
-// of 64; wave w takes items w, w + 16, ..., with its first two items' words
-// requested before the tables are built and, after that, the words of the
-// item two ahead requested as it sums one. Every load is issued
+// of 64; wave w takes items w, w + 16, ... (so each SIMD's four waves hold
+// equal shares), with its first item's words requested before the tables are
+// built and the next item's as it sums one. Every load is issued
 // unconditionally (past the end of a run a wave re-reads the item it sums,
 // from cache), so the compiler's wait counts stay exact: a wait for one item
 // never waits for the next.
@@ -1158,11 +1158,12 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // The first two items' words are in flight while the tables are built.
+    // The first item's words are in flight while the tables are built (a
+    // second item's too measured slower: with every CU's waves issuing, the
+    // issue itself waits for the memory queue, and the tables wait behind it).
     wait_vector_memory();
     uint32_t wa[kBlockWords], wb[kBlockWords];
     load(item_of(0), wa);
-    load(item_of(1), wb);
     TQ1_PHASE(strip_wave_id, 1);  // activations arrived, first words issued
 
     if constexpr (STAGE) {
@@ -1183,13 +1184,12 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
         if (t < RG) lds_f[geo.value_base + t] = half_bits_to_float(w[0]) * sum;
     };
     // No branch separates a load from the loop's other loads, so every path
-    // into the loop head carries the same fourteen loads in flight (wa's
-    // issued before wb's).
+    // into the loop head carries the same seven loads in flight.
     for (int j = 0; j < n_own; j += 2) {
+        load(item_of(j + 1), wb);
         consume(item_of(j), wa);
         load(item_of(j + 2), wa);
         if (j + 1 < n_own) consume(item_of(j + 1), wb);
-        load(item_of(j + 3), wb);
     }
     TQ1_PHASE(strip_wave_id, 3);  // all items summed
     __syncthreads();
