@@ -518,8 +518,12 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const uint32_t *__re
 // Illegal regular bytes index inside the group's 927 entries and the tail is
 // clamped, so no input reads outside the tables.
 // ---------------------------------------------------------------------------
-// Blocks whose words are in flight ahead of the one being consumed.
-constexpr int kLutLoadAhead = 2;
+// Blocks whose words are in flight ahead of the one being consumed, for a
+// wave stream of cb blocks per sub-chunk: one where the stream has two (the
+// second issued while the first is summed rather than before the tables:
+// gate/up M=1 9.64-9.74 -> 9.24-9.33 us on MI355X, O and out_proj the same),
+// two where it has more (down 10.16-10.23 against 10.24-10.32 with one).
+constexpr int lut_load_ahead(int cb) { return cb > 2 ? 2 : 1; }
 
 // The sub-chunk's activations (BT vectors x C groups), copied to LDS with
 // 16-byte loads (element loads for rows that are not 16-byte aligned): a
@@ -743,6 +747,7 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
     constexpr int RB = RT * kTileRows;  // rows per workgroup (threads per wave stream)
     constexpr int NT = RB * KW;
     constexpr int CB = C / KW;
+    constexpr int LA = lut_load_ahead(CB);
     __shared__ float lut[BT][C][kLutFloats];
     __shared__ __align__(16) T xs[BT][C * kBlockWeights];
     __shared__ float2 xchg[KW > 1 ? (KW - 1) * CB * BT : 1][RB];
@@ -778,8 +783,8 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
     // offsets as immediates) doubled the code for the same speed. Per sub-chunk
     // of C groups:
     //   1. the activations of this thread's table tasks, then this row's
-    //      blocks: only the first kLutLoadAhead blocks' words are issued before
-    //      the tables, block c + kLutLoadAhead as block c is consumed -- a wave
+    //      blocks: only the first LA blocks' words are issued before the
+    //      tables, block c + LA as block c is consumed -- a wave
     //      that issued all of its loads at once would stall on issue while the
     //      CU's memory queue drains, and reach its first sum only then;
     //   2. the tables, after every lane is done reading the previous ones;
@@ -798,7 +803,7 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
         const uint32_t *wp = row_words + (static_cast<int64_t>(g0) * kBlockWords + cb0 * kBlockWords) * kTileRows;
         uint32_t w[CB][kBlockWords];
 #pragma unroll
-        for (int c = 0; c < (kLutLoadAhead < CB ? kLutLoadAhead : CB); ++c)
+        for (int c = 0; c < (LA < CB ? LA : CB); ++c)
 #pragma unroll
             for (int j = 0; j < kBlockWords; ++j) w[c][j] = wp[(c * kBlockWords + j) * kTileRows];
         __builtin_amdgcn_sched_barrier(0);
@@ -812,10 +817,10 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
         if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 4);  // tables ready
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-            if (c + kLutLoadAhead < CB) {
+            if (c + LA < CB) {
 #pragma unroll
                 for (int j = 0; j < kBlockWords; ++j)
-                    w[c + kLutLoadAhead][j] = wp[((c + kLutLoadAhead) * kBlockWords + j) * kTileRows];
+                    w[c + LA][j] = wp[((c + LA) * kBlockWords + j) * kTileRows];
             }
             __builtin_amdgcn_sched_barrier(0);
             // The sum starts at slot 0's pair rather than at 0 + pair: equal
