@@ -1690,13 +1690,15 @@ __global__ __launch_bounds__(kDirectThreads, 3) void direct_gemm_kernel(
         // staged rows, 32 rows in windows of up to 4 groups and 64 in windows
         // of up to 2 (the planner's windows there): as 16-byte physical chunks
         // loaded into registers (8 per thread at 16 rows x 8 groups, 32 x 4 or
-        // 64 x 2) ahead of the first
-        // two word sets, each written to LDS after them as two 8-byte units at
-        // their K-order positions -- loads complete in order, so the writes
-        // wait for the activations only while the words are in flight.
-        // Otherwise by LDS-DMA (one padded row per instruction) waited for
-        // before any word is requested, as a second register pass would wait
-        // for the words too. (Measured on MI355X, gate/up: M=16 20.7 -> 19.0
+        // 64 x 2) ahead of the first word set, each written to LDS after it
+        // as two 8-byte units at their K-order positions -- loads complete in
+        // order, so the writes wait for the activations only while the words
+        // are in flight. Otherwise by LDS-DMA (one padded row per instruction)
+        // waited for before any word is requested, as a second register pass
+        // would wait for the words too. The second word set is requested after
+        // the staging barrier, so no wave reaches the barrier late for issuing
+        // it behind the CU's memory queue (M=8-32, every 27B shape, 1-3 %
+        // faster on MI355X). (Measured on MI355X, gate/up: M=16 20.7 -> 19.0
         // us and M=8 19.2 -> 18.3 us with 8-byte units in registers, 17.1 us
         // at M=8 with 16-byte chunks; M=32 in 8-group windows 27.8 us with
         // LDS-DMA against 32.4 with registers, 20.3 us in 4-group windows with
@@ -1733,7 +1735,6 @@ __global__ __launch_bounds__(kDirectThreads, 3) void direct_gemm_kernel(
             }
             __builtin_amdgcn_sched_barrier(0);
             load_chunk(wa, 0);
-            load_chunk(wb, CH);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int k = 0; k < kUnits / 2; ++k) {
@@ -1755,10 +1756,12 @@ __global__ __launch_bounds__(kDirectThreads, 3) void direct_gemm_kernel(
             }
             wait_vector_memory();
             load_chunk(wa, 0);
-            load_chunk(wb, CH);
         }
         if (w0 == 0) TQ1_PHASE(direct_wave_id, 1);  // first window's activations staged
         __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunk(wb, CH);
+        __builtin_amdgcn_sched_barrier(0);
 
         // Pipeline over the window (no barriers): MFMAs of group q interleaved
         // with the decode of q+1; words come in sets of four groups issued four
