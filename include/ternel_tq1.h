@@ -148,8 +148,14 @@ int ternel_tq1_tiled_from_words(const uint32_t *packed, int64_t rows, int64_t co
  * launch_tq1_lut23_smem_streamk, cuda/tq1_lut23_streamk.cu:336-367).
  * batch_tile in {1,2,4} (0 = auto); k_split divides columns/128 (0 = auto).
  * A split is reduced inside the same launch, in chunk order (deterministic).
+ * With M = 1 and both left automatic, a matrix of at most 40 groups per row
+ * whose rows give each CU a strip under 64 rows (QKV 8192 x 5120 on 256 CUs)
+ * runs a form that reduces every row inside one workgroup: no split, no
+ * workspace, bit-identical from run to run, equal to the split result to
+ * within fp32 reassociation of the per-group terms.
  * ws: at least ternel_tq1_matmul_workspace_bytes(...) bytes (0 when the split
- * resolves to 1; ws may then be NULL); see the workspace contract above.
+ * resolves to 1 or the form above runs; ws may then be NULL); see the
+ * workspace contract above.
  * A split batch whose (row block, batch tile) counters exceed the counter
  * region runs as several launches of as many rows as it holds, in order.
  */
