@@ -241,7 +241,7 @@ def main() -> int:
 
     import torch
 
-    from ternel_amd import synthetic
+    from ternel_amd import _lib, synthetic
     from ternel_amd.kernels import (GemmConfig, MatmulConfig, pack_weights, tq1_gemm_words, tq1_get_rows_words, tq1_linear_words,
                                     tq1_matmul_words, tq1_swiglu_words)
     from ternel_amd.layout import PackedTensorLayout
@@ -451,7 +451,10 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic["bytes_per_launch"] if traffic else None,
-            "kernel": f"{dom_name} GEMV K={dom_K} N={dom_N} (lut_gemv_kernel, fused ordered split-K)",
+            "kernel": f"{dom_name} GEMV K={dom_K} N={dom_N} ("
+                      + ("strip_gemv_kernel: every row reduced inside one workgroup, no split"
+                         if _lib.lib().ternel_tq1_matmul_workspace_bytes(1, dom_N, dom_K, 0, 0) == 0
+                         else "lut_gemv_kernel, fused ordered split-K") + ")",
             "bytes_per_launch": dom_bytes,
             "mean_launch_us": round(graph_launch_ms * 1e3, 3),
             "timing": f"{args.steps} cold launches back to back in one HIP graph, events on the launch stream",

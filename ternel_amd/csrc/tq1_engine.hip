@@ -948,10 +948,10 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // ---------------------------------------------------------------------------
 // strip_gemv_kernel: the M = 1 decode GEMV (one activation vector) for
 // matrices of at most kStripMaxGroups groups per row (K <= 5120) and at most
-// 62 rows per CU, with every row's K reduction inside one workgroup (the
+// 96 rows per CU, with every row's K reduction inside one workgroup (the
 // LUT23 algorithm of src/ternel_mlx/kernels.py:244-342).
 //
-// One workgroup per CU owns a strip of R < 64 rows: strip s holds rows
+// One workgroup per CU owns a strip of R <= 96 rows: strip s holds rows
 // [2 floor(s U / P), 2 floor((s + 1) U / P)), U = ceil(N / 2), so strips
 // differ by at most two rows and a gate/up pair never straddles two of them.
 // Workgroup b takes strip (b % 8) P / 8 + b / 8 when P is a multiple of 8:
@@ -971,18 +971,19 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // from cache), so the compiler's wait counts stay exact: a wait for one item
 // never waits for the next.
 // Sums: a block's in the reference's slot order; its scale * sum stored
-// alone; a row adds its G values in group order. The order is fixed by the
+// alone; a row adds its G values in group order, by lane i % 64 of wave i / 64
+// (SW waves: one for strips up to 64 rows, two above). The order is fixed by the
 // shape, so results are bit-identical from run to run, and equal the
 // reference's to within fp32 reassociation of the per-group terms.
 // No workspace, no memory shared between workgroups.
-// (Strips of 64 rows or more run the (tile, group) LUT23 kernel above:
-// rebuilding all G tables per CU there costs more than its fix-up.)
+// (Above 96 rows per CU the (tile, group) LUT23 kernel above runs: its 2-3
+// workgroups per CU overlap one workgroup's table build with another's sums,
+// which at more than 96 rows outweighs the split-K hand-off this avoids.)
 // ---------------------------------------------------------------------------
 constexpr int kStripWaves = 16;
 constexpr int kStripThreads = kStripWaves * 64;
 constexpr int kStripMaxGroups = 40;
-constexpr int kStripMaxRows = 62;
-constexpr int kStripSumWaves = (kStripMaxRows + 63) / 64;
+constexpr int kStripMaxRows = 96;
 constexpr int kStripLdsFloats = 40960;  // 160 KiB, the workgroup limit
 static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows <= kStripLdsFloats, "LDS fits");
 constexpr int kStripTrit3Iters = (kStripMaxGroups * (kFullSlots + 1) + kStripThreads - 1) / kStripThreads;
@@ -1101,7 +1102,7 @@ __device__ __forceinline__ void strip_store(T *__restrict__ y, int row, int lane
 // STAGE: the activations are a 2-byte type at a 16-byte aligned address and
 // are staged in LDS with one 16-byte load per thread; otherwise each thread
 // reads its table tasks' activations from global memory.
-template <typename T, bool GLU, bool STAGE>
+template <typename T, bool GLU, bool STAGE, int SW>
 __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint32_t *__restrict__ packed,
                                                                       const T *__restrict__ x, T *__restrict__ y,
                                                                       StripGeometry geo) {
@@ -1200,7 +1201,8 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     __syncthreads();
 
     // Row i by lane i % 64 of wave i / 64: its G block values in group order.
-    if (wave < kStripSumWaves) {
+    static_assert(SW == 1 || SW == 2, "one or two waves add the row sums");
+    if (wave < SW) {
         const int i = wave * 64 + lane;
         float total = 0.0f;
         if (i < R) {
@@ -3012,7 +3014,7 @@ int launch_lut_once(const uint32_t *packed, const void *x, void *y, int64_t M, i
 }
 
 // The M = 1 strip GEMV (strip_gemv_kernel): one workgroup per CU, at most
-// one per two rows, for strips below 64 rows and at most 40 groups.
+// one per two rows, for strips of at most 96 rows and at most 40 groups.
 int plan_strip(int64_t rows, int64_t columns, StripGeometry *geo) {
     const int64_t G = columns / kBlockWeights;
     if (G > kStripMaxGroups) return fail(TERNEL_TQ1_EINVAL, "the strip GEMV takes at most %d groups per row", kStripMaxGroups);
@@ -3038,14 +3040,23 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     const bool stage = sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     const T *xt = static_cast<const T *>(x);
     T *yt = static_cast<T *>(y);
-#define TQ1_STRIP_LAUNCH(STAGE)                                                                                   \
+    // Two waves add the row sums where a strip has more than 64 rows.
+    const bool two = 2 * ((geo.units + geo.P - 1) / geo.P) > 64;
+#define TQ1_STRIP_LAUNCH_SW(STAGE, SW)                                                                           \
     do {                                                                                                        \
         if (glu)                                                                                                \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE>), grid, dim3(kStripThreads), 0, stream, packed, \
-                               xt, yt, geo);                                                                   \
-        else                                                                                                    \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE>), grid, dim3(kStripThreads), 0, stream,       \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE, SW>), grid, dim3(kStripThreads), 0, stream,    \
                                packed, xt, yt, geo);                                                           \
+        else                                                                                                    \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, SW>), grid, dim3(kStripThreads), 0, stream,   \
+                               packed, xt, yt, geo);                                                           \
+    } while (0)
+#define TQ1_STRIP_LAUNCH(STAGE)              \
+    do {                                     \
+        if (two)                             \
+            TQ1_STRIP_LAUNCH_SW(STAGE, 2);   \
+        else                                 \
+            TQ1_STRIP_LAUNCH_SW(STAGE, 1);   \
     } while (0)
     if constexpr (sizeof(T) == 2) {
         if (stage) {
@@ -3056,6 +3067,7 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     }
     TQ1_STRIP_LAUNCH(false);
 #undef TQ1_STRIP_LAUNCH
+#undef TQ1_STRIP_LAUNCH_SW
     TQ1_LAUNCH_CHECK();
     return TERNEL_TQ1_OK;
 }

@@ -97,8 +97,8 @@ def test_fused_swiglu_gemv_at_the_27b_mlp_width() -> None:
 
 def test_split_gemv_on_two_streams_at_once() -> None:
     """Each stream has its own workspace: interleaved launches on two streams
-    give each stream's result exactly."""
-    rows, columns = 17408, 5120
+    give each stream's result exactly (down 17408 -> 5120, a 17-way split)."""
+    rows, columns = 5120, 17408
     blocks = [random_blocks(rows, columns, seed=s) for s in (21, 22)]
     xs = [np.random.default_rng(s).normal(0, 1, size=(1, columns)).astype(np.float16) for s in (21, 22)]
     packed = [pack(b) for b in blocks]

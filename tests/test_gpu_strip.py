@@ -1,4 +1,4 @@
-"""The strip GEMV (one activation vector, strips of at most 62 rows per CU, at
+"""The strip GEMV (one activation vector, strips of at most 96 rows per CU, at
 most 40 groups per row) against the oracle.
 
 The automatic configuration of ``tq1_matmul_words`` runs it for these shapes;
@@ -43,11 +43,12 @@ def run(blocks: np.ndarray, x: torch.Tensor) -> torch.Tensor:
 
 
 # (rows, columns): QKV (20 items of 64 blocks per strip: waves 0-3 sum two,
-# the rest one); 4096^2; one group; strips of 8 and 10 rows (2050 rows over 256
-# CUs) and an odd last strip; the 62-row edge (15872 rows); 12 groups; 16 items
-# per strip (one per wave).
-SHAPES = ((8192, 5120), (4096, 4096), (2048, 128), (2050, 640), (3001, 1024), (15872, 5120), (6144, 1536),
-          (8192, 4096))
+# the rest one); gate/up (68-row strips: two waves add the row sums); 4096^2;
+# one group; strips of 8 and 10 rows (2050 rows over 256 CUs) and an odd last
+# strip; 62, 64 (one summing wave's edge) and 66 rows; the 96-row edge (24576
+# rows); 12 groups; 16 items per strip (one per wave).
+SHAPES = ((8192, 5120), (17408, 5120), (4096, 4096), (2048, 128), (2050, 640), (3001, 1024), (15872, 5120),
+          (16384, 2560), (16896, 3072), (24576, 5120), (6144, 1536), (8192, 4096))
 
 
 @pytest.mark.parametrize(("rows", "columns"), SHAPES)
@@ -111,10 +112,11 @@ def test_results_are_bit_identical_from_run_to_run() -> None:
 
 
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
-def test_fused_swiglu_form(dtype) -> None:
-    """Rows alternate gate, up (12288 rows: 6144 units); the kernel writes
-    SiLU(gate) * up from the two outputs rounded to the activation type."""
-    rows, columns = 12288, 5120
+@pytest.mark.parametrize("rows", (12288, 20480))  # 48- and 80-row strips (one and two summing waves)
+def test_fused_swiglu_form(dtype, rows) -> None:
+    """Rows alternate gate, up; the kernel writes SiLU(gate) * up from the two
+    outputs rounded to the activation type."""
+    columns = 5120
     assert takes_strip(rows, columns)
     blocks = random_blocks(rows, columns, seed=23)
     x = to_dev(np.random.default_rng(23).normal(0.0, 1.0, size=(1, columns)).astype(np.float32)).to(dtype)

@@ -235,14 +235,15 @@ def test_workspace_queries() -> None:
     # every split workspace: a fixed 64 KiB counter region (its last word the
     # error word), then fp32 partials
     counters = 64 * 1024
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 17408, 5120, 0, 0) == counters + 10 * 17408 * 4
-    # one vector, strips of at most 62 rows (256 CUs without a GPU) and at most
+    # one vector, strips of at most 96 rows (256 CUs without a GPU) and at most
     # 40 groups: the strip GEMV, which needs no workspace
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 17408, 5120, 0, 0) == 0
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 17408, 5120, 1, 0) == counters + 10 * 17408 * 4
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 8192, 5120, 0, 0) == 0
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 4096, 4096, 0, 0) == 0
     assert handle.ternel_tq1_swiglu_workspace_bytes(1, 12288, 5120, 0) == 0
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 15872, 5120, 0, 0) == 0
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 15874, 5120, 0, 0) > 0  # 64-row strips: LUT23
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 24576, 5120, 0, 0) == 0
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 24578, 5120, 0, 0) > 0  # 98-row strips: LUT23
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 8192, 8192, 0, 0) > 0  # 64 groups: LUT23
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 17408, 0, 0) == counters + 17 * 5120 * 4
     assert handle.ternel_tq1_swiglu_workspace_bytes(1, 34816, 5120, 0) == counters + 10 * 34816 * 4
