@@ -149,7 +149,8 @@ int ternel_tq1_tiled_from_words(const uint32_t *packed, int64_t rows, int64_t co
  * batch_tile in {1,2,4} (0 = auto); k_split divides columns/128 (0 = auto).
  * A split is reduced inside the same launch, in chunk order (deterministic).
  * With M = 1 and both left automatic, a matrix of at most 40 groups per row
- * whose rows give each CU a strip under 64 rows (QKV 8192 x 5120 on 256 CUs)
+ * whose rows give each CU a strip of at most 96 rows (QKV 8192 x 5120 and
+ * gate/up 17408 x 5120 on 256 CUs)
  * runs a form that reduces every row inside one workgroup: no split, no
  * workspace, bit-identical from run to run, equal to the split result to
  * within fp32 reassociation of the per-group terms.
