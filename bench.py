@@ -537,7 +537,7 @@ def main() -> int:
 
 PHASES = ("start", "activations arrived", "first words issued", "own tables written", "tables ready (barrier)",
           "blocks summed", "partial stored and acknowledged", "arrival counted", "fix-up done")
-# The strip GEMV's stamps (M=1 where a CU's share of the rows is below 64: QKV).
+# The strip GEMV's stamps (M=1 where a CU's strip is at most 96 rows and K <= 5120: gate/up, QKV).
 STRIP_PHASES = ("start", "activations arrived, first words issued", "tables ready", "all items summed", "done")
 # The wide form's stamps in the same slots (2-4 unused; 7 and 8 only where it reduces a shared tile).
 WIDE_PHASES = ("start", "first unit's operands in LDS", "-", "-", "-", "segment summed", "arrival counted",
