@@ -957,9 +957,10 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // Workgroup b takes strip (b % 8) P / 8 + b / 8 when P is a multiple of 8:
 // workgroups are dealt to the eight XCDs in turn, so each XCD holds adjacent
 // strips and a cache line shared by two strips is read into one L2.
-// The workgroup stages the activations in LDS (one 16-byte load per thread,
-// waited for before any weight word is requested: behind the chip-wide
-// burst of word loads they came back ~2 us later) and builds the LUT23
+// The workgroup stages the activations in LDS (one 16-byte load per thread;
+// no wave requests a weight word until every wave's activations are in LDS,
+// as a wave's activation load queued behind its CU's word loads comes back
+// microseconds later) and builds the LUT23
 // tables of all G groups once (G x 927 floats, 148,320 bytes at G = 40);
 // they stay for the whole launch, so a lane may look up any group. The
 // strip's R x G blocks are numbered t = g R + i (row i, group g), so
@@ -1155,47 +1156,57 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     };
     // (The scheduling barriers keep the sums of the item before from moving
     // above the loads, where they would wait for that item's words first.)
-    auto load = [&](int item, uint32_t (&w)[kBlockWords]) __attribute__((always_inline)) {
-        int t, g;
-        const uint32_t *p = packed + block(item, t, g);
+    // An item in flight: this lane's block words, its block index t and its
+    // group's table byte offset (computed once, at the load).
+    struct Item {
+        uint32_t w[kBlockWords];
+        int t;
+        uint32_t table;
+    };
+    auto load = [&](int item, Item &it) __attribute__((always_inline)) {
+        int g;
+        const uint32_t *p = packed + block(item, it.t, g);
+        it.table = mul_u24(static_cast<uint32_t>(g), kLutFloats * 4);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < kBlockWords; ++j) w[j] = p[j * kTileRows];
+        for (int j = 0; j < kBlockWords; ++j) it.w[j] = p[j * kTileRows];
         __builtin_amdgcn_sched_barrier(0);
     };
 
     // The first item's words are in flight while the tables are built (a
     // second item's too measured slower: with every CU's waves issuing, the
     // issue itself waits for the memory queue, and the tables wait behind it).
+    // With staged activations they are requested after the staging barrier,
+    // so no wave's activation load waits behind its CU's first words.
     wait_vector_memory();
-    uint32_t wa[kBlockWords], wb[kBlockWords];
-    load(item_of(0), wa);
-    TQ1_PHASE(strip_wave_id, 1);  // activations arrived, first words issued
-
+    Item wa, wb;
     if constexpr (STAGE) {
         T *const xs = reinterpret_cast<T *>(lds_f + geo.value_base);
         if (tid < pieces) reinterpret_cast<uint4 *>(xs)[tid] = piece;
         __syncthreads();
+        load(item_of(0), wa);
+        TQ1_PHASE(strip_wave_id, 1);  // activations arrived, first words issued
         tasks.gather(xs, G, tid);
+    } else {
+        load(item_of(0), wa);
+        TQ1_PHASE(strip_wave_id, 1);  // activations arrived, first words issued
     }
     tasks.build(lds_f, G, tid);
     __syncthreads();
     TQ1_PHASE(strip_wave_id, 2);  // tables ready
 
     const char *const lds = reinterpret_cast<const char *>(lds_f);
-    auto consume = [&](int item, const uint32_t (&w)[kBlockWords]) __attribute__((always_inline)) {
-        int t, g;
-        (void)block(item, t, g);
-        const float sum = strip_block_sum(w, lds, mul_u24(static_cast<uint32_t>(g), kLutFloats * 4));
-        if (t < RG) lds_f[geo.value_base + t] = half_bits_to_float(w[0]) * sum;
+    auto consume = [&](const Item &it) __attribute__((always_inline)) {
+        const float sum = strip_block_sum(it.w, lds, it.table);
+        if (it.t < RG) lds_f[geo.value_base + it.t] = half_bits_to_float(it.w[0]) * sum;
     };
     // No branch separates a load from the loop's other loads, so every path
     // into the loop head carries the same seven loads in flight.
     for (int j = 0; j < n_own; j += 2) {
         load(item_of(j + 1), wb);
-        consume(item_of(j), wa);
+        consume(wa);
         load(item_of(j + 2), wa);
-        if (j + 1 < n_own) consume(item_of(j + 1), wb);
+        if (j + 1 < n_own) consume(wb);
     }
     TQ1_PHASE(strip_wave_id, 3);  // all items summed
     __syncthreads();
