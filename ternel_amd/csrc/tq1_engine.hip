@@ -972,10 +972,11 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // from cache), so the compiler's wait counts stay exact: a wait for one item
 // never waits for the next.
 // Sums: a block's in the reference's slot order; its scale * sum stored
-// alone; a row adds its G values in group order, by lane i % 64 of wave i / 64
-// (SW waves: one for strips up to 64 rows, two above). The order is fixed by the
-// shape, so results are bit-identical from run to run, and equal the
-// reference's to within fp32 reassociation of the per-group terms.
+// alone; a row's G values in four contiguous group ranges, each in group order
+// by one lane of a quad, and the four partials added across the quad with lane
+// swaps. The order is fixed by the shape, so results are bit-identical from
+// run to run, and equal the reference's to within fp32 reassociation of the
+// per-group terms.
 // No workspace, no memory shared between workgroups.
 // (Above 96 rows per CU the (tile, group) LUT23 kernel above runs: its 2-3
 // workgroups per CU overlap one workgroup's table build with another's sums,
@@ -1089,21 +1090,10 @@ __device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords
     return sum + at(table + 4 * tq1_bytes::tail_entry(w[6] >> 24), kTailBase);
 }
 
-template <typename T, bool GLU>
-__device__ __forceinline__ void strip_store(T *__restrict__ y, int row, int lane, bool valid, float v) {
-    if constexpr (GLU) {
-        const T own = from_f32<T>(v);
-        const float partner = __shfl_xor(to_f32<T>(own), 1, 64);
-        if (valid && (lane & 1) == 0) y[row / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
-    } else {
-        if (valid) y[row] = from_f32<T>(v);
-    }
-}
-
 // STAGE: the activations are a 2-byte type at a 16-byte aligned address and
 // are staged in LDS with one 16-byte load per thread; otherwise each thread
 // reads its table tasks' activations from global memory.
-template <typename T, bool GLU, bool STAGE, int SW>
+template <typename T, bool GLU, bool STAGE>
 __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint32_t *__restrict__ packed,
                                                                       const T *__restrict__ x, T *__restrict__ y,
                                                                       StripGeometry geo) {
@@ -1211,17 +1201,30 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     TQ1_PHASE(strip_wave_id, 3);  // all items summed
     __syncthreads();
 
-    // Row i by lane i % 64 of wave i / 64: its G block values in group order.
-    static_assert(SW == 1 || SW == 2, "one or two waves add the row sums");
-    if (wave < SW) {
-        const int i = wave * 64 + lane;
-        float total = 0.0f;
+    // Row i by the four lanes 4i .. 4i + 3 (threads 4i + q): lane q adds the
+    // values of groups [qG/4, (q + 1)G/4) in group order (-0, the identity of
+    // +, for an empty range), then the quad adds its four partials pairwise
+    // across lanes with DPP, (p0 + p1) + (p2 + p3), which every lane of the
+    // quad computes to the same value. The order is fixed by the shape.
+    if (wave < (4 * R + 63) >> 6) {
+        const int i = tid >> 2, q = tid & 3;
+        float part = -0.0f;
         if (i < R) {
             const float *v = lds_f + geo.value_base + i;
-            total = v[0];
-            for (int g = 1; g < G; ++g) total += v[g * R];
+            const int g1 = ((q + 1) * G) >> 2;
+            for (int g = (q * G) >> 2; g < g1; ++g) part += v[g * R];
         }
-        strip_store<T, GLU>(y, lo + i, lane, i < R, total);
+        // DPP quad permutes: [1, 0, 3, 2] swaps neighbours, [2, 3, 0, 1] pairs.
+        const float pair = part + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part), 0xb1, 0xf, 0xf, false));
+        const float total = pair + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pair), 0x4e, 0xf, 0xf, false));
+        if constexpr (GLU) {
+            // Rows 2r and 2r + 1 (lo is even) sit four lanes apart.
+            const T own = from_f32<T>(total);
+            const float partner = __shfl_xor(to_f32<T>(own), 4, 64);
+            if (i < R && (tid & 7) == 0) y[(lo + i) / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
+        } else {
+            if (i < R && q == 0) y[lo + i] = from_f32<T>(total);
+        }
     }
     TQ1_PHASE(strip_wave_id, 4);  // done
 }
@@ -3051,23 +3054,14 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     const bool stage = sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     const T *xt = static_cast<const T *>(x);
     T *yt = static_cast<T *>(y);
-    // Two waves add the row sums where a strip has more than 64 rows.
-    const bool two = 2 * ((geo.units + geo.P - 1) / geo.P) > 64;
-#define TQ1_STRIP_LAUNCH_SW(STAGE, SW)                                                                           \
+#define TQ1_STRIP_LAUNCH(STAGE)                                                                                 \
     do {                                                                                                        \
         if (glu)                                                                                                \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE, SW>), grid, dim3(kStripThreads), 0, stream,    \
-                               packed, xt, yt, geo);                                                           \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE>), grid, dim3(kStripThreads), 0, stream, packed, \
+                               xt, yt, geo);                                                                   \
         else                                                                                                    \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, SW>), grid, dim3(kStripThreads), 0, stream,   \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE>), grid, dim3(kStripThreads), 0, stream,       \
                                packed, xt, yt, geo);                                                           \
-    } while (0)
-#define TQ1_STRIP_LAUNCH(STAGE)              \
-    do {                                     \
-        if (two)                             \
-            TQ1_STRIP_LAUNCH_SW(STAGE, 2);   \
-        else                                 \
-            TQ1_STRIP_LAUNCH_SW(STAGE, 1);   \
     } while (0)
     if constexpr (sizeof(T) == 2) {
         if (stage) {
@@ -3078,7 +3072,6 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     }
     TQ1_STRIP_LAUNCH(false);
 #undef TQ1_STRIP_LAUNCH
-#undef TQ1_STRIP_LAUNCH_SW
     TQ1_LAUNCH_CHECK();
     return TERNEL_TQ1_OK;
 }
