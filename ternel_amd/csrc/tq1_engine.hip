@@ -972,9 +972,9 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // from cache), so the compiler's wait counts stay exact: a wait for one item
 // never waits for the next.
 // Sums: a block's in the reference's slot order; its scale * sum stored
-// alone; a row's G values in four contiguous group ranges, each in group order
-// by one lane of a quad, and the four partials added across the quad with lane
-// swaps. The order is fixed by the shape, so results are bit-identical from
+// alone; a row's G values in eight contiguous group ranges, each in group
+// order by one of eight adjacent lanes, and the eight partials added across
+// the lanes with DPP. The order is fixed by the shape, so results are bit-identical from
 // run to run, and equal the reference's to within fp32 reassociation of the
 // per-group terms.
 // No workspace, no memory shared between workgroups.
@@ -1201,27 +1201,31 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     TQ1_PHASE(strip_wave_id, 3);  // all items summed
     __syncthreads();
 
-    // Row i by the four lanes 4i .. 4i + 3 (threads 4i + q): lane q adds the
-    // values of groups [qG/4, (q + 1)G/4) in group order (-0, the identity of
-    // +, for an empty range), then the quad adds its four partials pairwise
-    // across lanes with DPP, (p0 + p1) + (p2 + p3), which every lane of the
-    // quad computes to the same value. The order is fixed by the shape.
-    if (wave < (4 * R + 63) >> 6) {
-        const int i = tid >> 2, q = tid & 3;
+    // Row i by the eight lanes 8i .. 8i + 7 (threads 8i + q): lane q adds the
+    // values of groups [qG/8, (q + 1)G/8) in group order (-0, the identity of
+    // +, for an empty range), then the eight partials are added pairwise
+    // across lanes with DPP, ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)):
+    // quad permutes within each half, then the upper half's sum shifted down
+    // four lanes within the row of 16. Lane 8i holds the total. The order is
+    // fixed by the shape.
+    if (wave < (8 * R + 63) >> 6) {
+        const int i = tid >> 3, q = tid & 7;
         float part = -0.0f;
         if (i < R) {
             const float *v = lds_f + geo.value_base + i;
-            const int g1 = ((q + 1) * G) >> 2;
-            for (int g = (q * G) >> 2; g < g1; ++g) part += v[g * R];
+            const int g1 = ((q + 1) * G) >> 3;
+            for (int g = (q * G) >> 3; g < g1; ++g) part += v[g * R];
         }
-        // DPP quad permutes: [1, 0, 3, 2] swaps neighbours, [2, 3, 0, 1] pairs.
+        // DPP: quad_perm [1, 0, 3, 2] swaps neighbours, [2, 3, 0, 1] pairs,
+        // row_shl:4 (0x104) reads the lane four above.
         const float pair = part + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part), 0xb1, 0xf, 0xf, false));
-        const float total = pair + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pair), 0x4e, 0xf, 0xf, false));
+        const float quad = pair + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pair), 0x4e, 0xf, 0xf, false));
+        const float total = quad + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(quad), 0x104, 0xf, 0xf, false));
         if constexpr (GLU) {
-            // Rows 2r and 2r + 1 (lo is even) sit four lanes apart.
+            // Rows 2r and 2r + 1 (lo is even) sit eight lanes apart.
             const T own = from_f32<T>(total);
-            const float partner = __shfl_xor(to_f32<T>(own), 4, 64);
-            if (i < R && (tid & 7) == 0) y[(lo + i) / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
+            const float partner = __shfl_xor(to_f32<T>(own), 8, 64);
+            if (i < R && (tid & 15) == 0) y[(lo + i) / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
         } else {
             if (i < R && q == 0) y[lo + i] = from_f32<T>(total);
         }
