@@ -668,24 +668,30 @@ __device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
     return r;
 }
 
-__device__ __forceinline__ void split_pair(uint32_t pair, uint32_t base, uint32_t &lo_a, uint32_t &hi_a,
-                                           uint32_t &lo_b, uint32_t &hi_b) {
+__device__ __forceinline__ void split_pair(uint32_t pair, uint32_t base_lo, uint32_t base_hi, uint32_t &lo_a,
+                                           uint32_t &hi_a, uint32_t &lo_b, uint32_t &hi_b) {
     const u16x2 p = __builtin_bit_cast(u16x2, pair);
     const u16x2 h = tq1_bytes::lut23_high(p);
     const u16x2 l = tq1_bytes::lut23_low(p, h);
     const uint32_t hb = __builtin_bit_cast(uint32_t, h), lb = __builtin_bit_cast(uint32_t, l);
-    lo_a = lut_address_lo(lb, base);
-    hi_a = lut_address_lo(hb, base);
-    lo_b = lut_address_hi(lb, base);
-    hi_b = lut_address_hi(hb, base);
+    lo_a = lut_address_lo(lb, base_lo);
+    hi_a = lut_address_lo(hb, base_hi);
+    lo_b = lut_address_hi(lb, base_lo);
+    hi_b = lut_address_hi(hb, base_hi);
 }
 
 // All four bytes of a block word: table byte addresses lo/hi for byte b of the
 // word. Bytes 1 and 3 move to the 16-bit halves with one byte permute
-// (selector 0x0c = zero).
+// (selector 0x0c = zero). The two-trit digits index from base_lo, the
+// three-trit ones from base_hi.
+__device__ __forceinline__ void split_word(uint32_t word, uint32_t base_lo, uint32_t base_hi, uint32_t (&lo)[4],
+                                           uint32_t (&hi)[4]) {
+    split_pair(word & 0x00ff00ffu, base_lo, base_hi, lo[0], hi[0], lo[2], hi[2]);  // bytes 0 and 2
+    split_pair(__builtin_amdgcn_perm(0u, word, 0x0c030c01u), base_lo, base_hi, lo[1], hi[1], lo[3],
+               hi[3]);  // bytes 1 and 3
+}
 __device__ __forceinline__ void split_word(uint32_t word, uint32_t base, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
-    split_pair(word & 0x00ff00ffu, base, lo[0], hi[0], lo[2], hi[2]);                           // bytes 0 and 2
-    split_pair(__builtin_amdgcn_perm(0u, word, 0x0c030c01u), base, lo[1], hi[1], lo[3], hi[3]);  // bytes 1 and 3
+    split_word(word, base, base, lo, hi);
 }
 
 // Adds partial[0..k) (stride apart) left to right. The agent-coherent loads of
@@ -987,6 +993,14 @@ constexpr int kStripThreads = kStripWaves * 64;
 constexpr int kStripMaxGroups = 40;
 constexpr int kStripMaxRows = 96;
 constexpr int kStripLdsFloats = 40960;  // 160 KiB, the workgroup limit
+// The tables of all groups in two regions: every group's 26 three-trit
+// tables (27 floats each, the tail last) from float 0, then every group's 25
+// two-trit tables (9 floats each). Task k of a kind writes at k times its
+// table size, so a wave's 64 consecutive tasks start in 64 different banks
+// (27 and 9 are odd).
+constexpr int kStripL3Floats = (kFullSlots + 1) * kL3Entries;  // 702 per group
+constexpr int kStripL2Floats = kFullSlots * kL2Entries;        // 225 per group
+static_assert(kStripL3Floats + kStripL2Floats == kLutFloats, "the regions hold every group's 927 floats");
 static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows <= kStripLdsFloats, "LDS fits");
 constexpr int kStripTrit3Iters = (kStripMaxGroups * (kFullSlots + 1) + kStripThreads - 1) / kStripThreads;
 constexpr int kStripL2Iters = (kStripMaxGroups * kFullSlots + kStripThreads - 1) / kStripThreads;
@@ -1009,7 +1023,8 @@ __device__ __forceinline__ int strip_row(int s, const StripGeometry &geo) {
 // slot t % 26; slot 25 the tail), two-trit task t < 25 G is (group t / 25,
 // slot t % 25). gather() reads their activations (from LDS or global memory,
 // every read issued, indices clamped), build() writes the tables from them,
-// as build_lut_tables computes them.
+// as build_lut_tables computes them, task t of a kind at t times its table
+// size in that kind's region.
 template <typename T>
 struct StripTasks {
     T v3[kStripTrit3Iters][3], v2[kStripL2Iters][2];
@@ -1039,7 +1054,6 @@ struct StripTasks {
         for (int it = 0; it < kStripTrit3Iters; ++it) {
             const int t = tid + it * kStripThreads;
             if (t < G * (kFullSlots + 1)) {
-                const int g = t / (kFullSlots + 1), s = t - g * (kFullSlots + 1);
                 const float x0 = to_f32<T>(v3[it][0]), x1 = to_f32<T>(v3[it][1]), x2 = to_f32<T>(v3[it][2]);
                 const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
                 const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
@@ -1047,7 +1061,7 @@ struct StripTasks {
                 float pair[kL2Entries];
 #pragma unroll
                 for (int e = 0; e < kL2Entries; ++e) pair[e] = a[e % 3] + b[e / 3];
-                float *dst = lut + g * kLutFloats + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
+                float *dst = lut + t * kL3Entries;  // the three-trit region's g * 702 + 27 s
 #pragma unroll
                 for (int e = 0; e < kL3Entries; ++e) dst[e] = pair[e % 9] + d[e / 9];
             }
@@ -1056,11 +1070,10 @@ struct StripTasks {
         for (int it = 0; it < kStripL2Iters; ++it) {
             const int t = tid + it * kStripThreads;
             if (t < G * kFullSlots) {
-                const int g = t / kFullSlots, s = t - g * kFullSlots;
                 const float x0 = to_f32<T>(v2[it][0]), x1 = to_f32<T>(v2[it][1]);
                 const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
                 const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
-                float *dst = lut + g * kLutFloats + s * kL2Entries;
+                float *dst = lut + G * kStripL3Floats + t * kL2Entries;  // the two-trit region's g * 225 + 9 s
 #pragma unroll
                 for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
             }
@@ -1068,9 +1081,11 @@ struct StripTasks {
     }
 };
 
-// One block's LUT23 sum from its words and its group's tables at byte
-// offset `table`: slot 0..24 in order, then the tail (the reference's order).
-__device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords], const char *lds, uint32_t table) {
+// One block's LUT23 sum from its words and its group's two-trit and
+// three-trit tables at byte offsets `table2` and `table3`: slot 0..24 in
+// order, then the tail (the reference's order).
+__device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords], const char *lds, uint32_t table2,
+                                                 uint32_t table3) {
     auto at = [&](uint32_t address, int entry) {
         return *reinterpret_cast<const float *>(lds + address + entry * 4);
     };
@@ -1078,16 +1093,16 @@ __device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords
 #pragma unroll
     for (int word = 0; word < kBlockWords; ++word) {
         uint32_t lo[4], hi[4];
-        split_word(w[word], table, lo, hi);
+        split_word(w[word], table2, table3, lo, hi);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
             if (s < 0 || s >= kFullSlots) continue;
-            const float pair = at(lo[b], s * kL2Entries) + at(hi[b], kL3Base + s * kL3Entries);
+            const float pair = at(lo[b], s * kL2Entries) + at(hi[b], s * kL3Entries);
             sum = s == 0 ? pair : sum + pair;
         }
     }
-    return sum + at(table + 4 * tq1_bytes::tail_entry(w[6] >> 24), kTailBase);
+    return sum + at(table3 + 4 * tq1_bytes::tail_entry(w[6] >> 24), kFullSlots * kL3Entries);
 }
 
 // STAGE: the activations are a 2-byte type at a 16-byte aligned address and
@@ -1151,12 +1166,13 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     struct Item {
         uint32_t w[kBlockWords];
         int t;
-        uint32_t table;
+        uint32_t table2, table3;
     };
     auto load = [&](int item, Item &it) __attribute__((always_inline)) {
         int g;
         const uint32_t *p = packed + block(item, it.t, g);
-        it.table = mul_u24(static_cast<uint32_t>(g), kLutFloats * 4);
+        it.table3 = mul_u24(static_cast<uint32_t>(g), kStripL3Floats * 4);
+        it.table2 = mad_u24(static_cast<uint32_t>(g), kStripL2Floats * 4, static_cast<uint32_t>(G * kStripL3Floats * 4));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < kBlockWords; ++j) it.w[j] = p[j * kTileRows];
@@ -1187,7 +1203,7 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
 
     const char *const lds = reinterpret_cast<const char *>(lds_f);
     auto consume = [&](const Item &it) __attribute__((always_inline)) {
-        const float sum = strip_block_sum(it.w, lds, it.table);
+        const float sum = strip_block_sum(it.w, lds, it.table2, it.table3);
         if (it.t < RG) lds_f[geo.value_base + it.t] = half_bits_to_float(it.w[0]) * sum;
     };
     // No branch separates a load from the loop's other loads, so every path
