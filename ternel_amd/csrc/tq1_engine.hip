@@ -1108,7 +1108,7 @@ __device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords
 // STAGE: the activations are a 2-byte type at a 16-byte aligned address and
 // are staged in LDS with one 16-byte load per thread; otherwise each thread
 // reads its table tasks' activations from global memory.
-template <typename T, bool GLU, bool STAGE>
+template <typename T, bool GLU, bool STAGE, int PAIRS>
 __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint32_t *__restrict__ packed,
                                                                       const T *__restrict__ x, T *__restrict__ y,
                                                                       StripGeometry geo) {
@@ -1206,12 +1206,15 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
         const float sum = strip_block_sum(it.w, lds, it.table2, it.table3);
         if (it.t < RG) lds_f[geo.value_base + it.t] = half_bits_to_float(it.w[0]) * sum;
     };
-    // No branch separates a load from the loop's other loads, so every path
-    // into the loop head carries the same seven loads in flight.
-    for (int j = 0; j < n_own; j += 2) {
+    // A wave owns at most 2 PAIRS items (the launcher picks PAIRS from the
+    // strip shape), so the loop unrolls completely; the last pair requests
+    // nothing after it. Loads are issued whether or not their item is summed.
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+        const int j = 2 * p;
         load(item_of(j + 1), wb);
-        consume(wa);
-        load(item_of(j + 2), wa);
+        if (j < n_own) consume(wa);
+        if (p + 1 < PAIRS) load(item_of(j + 2), wa);
         if (j + 1 < n_own) consume(wb);
     }
     TQ1_PHASE(strip_wave_id, 3);  // all items summed
@@ -3074,14 +3077,26 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     const bool stage = sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     const T *xt = static_cast<const T *>(x);
     T *yt = static_cast<T *>(y);
-#define TQ1_STRIP_LAUNCH(STAGE)                                                                                 \
+    // Items per wave: the largest strip's ceil(R G / 64) items over 16 waves.
+    const int64_t max_rows = 2 * ((geo.units + geo.P - 1) / geo.P);
+    const int64_t per_wave = ceil_div(ceil_div(max_rows * geo.G, 64), kStripWaves);
+    if (per_wave > 4) return fail(TERNEL_TQ1_EINVAL, "strip of %lld items per wave", static_cast<long long>(per_wave));
+    const bool two_pairs = per_wave > 2;
+#define TQ1_STRIP_LAUNCH_P(STAGE, PAIRS)                                                                        \
     do {                                                                                                        \
         if (glu)                                                                                                \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE>), grid, dim3(kStripThreads), 0, stream, packed, \
-                               xt, yt, geo);                                                                   \
-        else                                                                                                    \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE>), grid, dim3(kStripThreads), 0, stream,       \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE, PAIRS>), grid, dim3(kStripThreads), 0, stream, \
                                packed, xt, yt, geo);                                                           \
+        else                                                                                                    \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, PAIRS>), grid, dim3(kStripThreads), 0, stream,\
+                               packed, xt, yt, geo);                                                           \
+    } while (0)
+#define TQ1_STRIP_LAUNCH(STAGE)               \
+    do {                                      \
+        if (two_pairs)                        \
+            TQ1_STRIP_LAUNCH_P(STAGE, 2);     \
+        else                                  \
+            TQ1_STRIP_LAUNCH_P(STAGE, 1);     \
     } while (0)
     if constexpr (sizeof(T) == 2) {
         if (stage) {
@@ -3092,6 +3107,7 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     }
     TQ1_STRIP_LAUNCH(false);
 #undef TQ1_STRIP_LAUNCH
+#undef TQ1_STRIP_LAUNCH_P
     TQ1_LAUNCH_CHECK();
     return TERNEL_TQ1_OK;
 }
