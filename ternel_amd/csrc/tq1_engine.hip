@@ -60,6 +60,11 @@ using tq1_bytes::kL3Entries;
 using tq1_bytes::kL3Base;
 using tq1_bytes::kTailBase;
 using tq1_bytes::kLutFloats;
+// The kernels lay a set of tables out in two regions (three-trit, then
+// two-trit): these are one group's share of each.
+constexpr int kLut3Floats = (tq1_bytes::kFullSlots + 1) * kL3Entries;  // 702: 25 slots and the tail
+constexpr int kLut2Floats = tq1_bytes::kFullSlots * kL2Entries;        // 225
+static_assert(kLut3Floats + kLut2Floats == kLutFloats, "the regions hold a group's 927 floats");
 
 constexpr int kThreads = 256;
 
@@ -593,9 +598,12 @@ struct ActivationCopy {
 // entry e = pair[e % 9] + d[e / 9] -- the reference's (a + b) + d, rounded
 // the same way. Entries are (t - 1) * x as real products, so 0 * inf = NaN
 // propagates as in the reference.
+// The tables lie in two regions: the BT C three-trit table sets (26 tables
+// of 27 floats each, 702 floats per (vector, group)) from float 0, then the
+// BT C two-trit sets (25 of 9 floats, 225). Task k of a kind writes at k
+// times its table size, so a wave's consecutive tasks start in distinct banks.
 template <typename T, int C, int BT, int NT>
-__device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats], const T (*xs)[C * kBlockWeights],
-                                                 int tid) {
+__device__ __forceinline__ void build_lut_tables(float *lut, const T (*xs)[C * kBlockWeights], int tid) {
     constexpr int kTrit3 = BT * C * (kFullSlots + 1);
     constexpr int kL2Start = (kTrit3 + 63) / 64 * 64;
     constexpr int kTasks = kL2Start + BT * C * kFullSlots;
@@ -615,7 +623,7 @@ __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats], co
             float pair[kL2Entries];
 #pragma unroll
             for (int e = 0; e < kL2Entries; ++e) pair[e] = a[e % 3] + b[e / 3];
-            float *dst = lut[j][c] + (s < kFullSlots ? kL3Base + s * kL3Entries : kTailBase);
+            float *dst = lut + i * kL3Entries;  // (j C + c) 702 + 27 s, the tail as slot 25
 #pragma unroll
             for (int e = 0; e < kL3Entries; ++e) dst[e] = pair[e % 9] + d[e / 9];
         } else if (i >= kL2Start && i < kTasks) {
@@ -628,7 +636,7 @@ __device__ __forceinline__ void build_lut_tables(float (*lut)[C][kLutFloats], co
             const float x0 = to_f32<T>(xg[0]), x1 = to_f32<T>(xg[1]);
             const float a[3] = {-1.0f * x0, 0.0f * x0, 1.0f * x0};
             const float b[3] = {-1.0f * x1, 0.0f * x1, 1.0f * x1};
-            float *dst = lut[j][c] + s * kL2Entries;
+            float *dst = lut + BT * C * kLut3Floats + t * kL2Entries;  // then (j C + c) 225 + 9 s
 #pragma unroll
             for (int e = 0; e < kL2Entries; ++e) dst[e] = a[e % 3] + b[e / 3];
         }
@@ -801,9 +809,15 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
     //      and scales in LDS; stream 0 folds them after a barrier.
     const int cb0 = stream * CB;  // first block of this wave's stream
     const char *const lut_bytes = reinterpret_cast<const char *>(&lut[0][0][0]);
-    const uint32_t lut_base = static_cast<uint32_t>(cb0 * kLutFloats * 4);
-    auto table = [&](uint32_t address, int j, int c, int entry) {
-        return *reinterpret_cast<const float *>(lut_bytes + address + ((j * C + c) * kLutFloats + entry) * 4);
+    // This stream's first three-trit and two-trit table sets (build_lut_tables'
+    // two regions).
+    const uint32_t base3 = static_cast<uint32_t>(cb0 * kLut3Floats * 4);
+    const uint32_t base2 = static_cast<uint32_t>((BT * C * kLut3Floats + cb0 * kLut2Floats) * 4);
+    auto table3 = [&](uint32_t address, int j, int c, int entry) {
+        return *reinterpret_cast<const float *>(lut_bytes + address + ((j * C + c) * kLut3Floats + entry) * 4);
+    };
+    auto table2 = [&](uint32_t address, int j, int c, int entry) {
+        return *reinterpret_cast<const float *>(lut_bytes + address + ((j * C + c) * kLut2Floats + entry) * 4);
     };
     auto run = [&](int g0) {
         const uint32_t *wp = row_words + (static_cast<int64_t>(g0) * kBlockWords + cb0 * kBlockWords) * kTileRows;
@@ -817,7 +831,7 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
         // (With several streams the fold barrier below already orders the
         // previous sub-chunk's table and exchange reads before this.)
         if (KW == 1 && g0 != g_begin) __syncthreads();
-        build_lut_tables<T, C, BT, NT>(lut, xs, tid);
+        build_lut_tables<T, C, BT, NT>(&lut[0][0][0], xs, tid);
         if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 3);  // own table entries written
         __syncthreads();
         if (g0 == g_begin) TQ1_PHASE(lut_wave_id, 4);  // tables ready
@@ -836,7 +850,7 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 #pragma unroll
             for (int word = 0; word < kBlockWords; ++word) {
                 uint32_t lo[4], hi[4];
-                split_word(w[c][word], lut_base, lo, hi);
+                split_word(w[c][word], base2, base3, lo, hi);
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
                     const int s = word * 4 + b - 2;  // code byte s is block byte 2 + s
@@ -844,16 +858,16 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 #pragma unroll
                     for (int j = 0; j < BT; ++j) {
                         const float pair =
-                            table(lo[b], j, c, s * kL2Entries) + table(hi[b], j, c, kL3Base + s * kL3Entries);
+                            table2(lo[b], j, c, s * kL2Entries) + table3(hi[b], j, c, s * kL3Entries);
                         sum[j] = s == 0 ? pair : sum[j] + pair;
                     }
                 }
             }
             const float scale = half_bits_to_float(w[c][0]);
-            const uint32_t tail = lut_base + 4 * tq1_bytes::tail_entry(w[c][6] >> 24);
+            const uint32_t tail = base3 + 4 * tq1_bytes::tail_entry(w[c][6] >> 24);
 #pragma unroll
             for (int j = 0; j < BT; ++j) {
-                sum[j] += table(tail, j, c, kTailBase);
+                sum[j] += table3(tail, j, c, kFullSlots * kL3Entries);
                 if (KW == 1 || stream == 0)
                     acc[j] = fmaf(scale, sum[j], acc[j]);
                 else
@@ -998,9 +1012,8 @@ constexpr int kStripLdsFloats = 40960;  // 160 KiB, the workgroup limit
 // two-trit tables (9 floats each). Task k of a kind writes at k times its
 // table size, so a wave's 64 consecutive tasks start in 64 different banks
 // (27 and 9 are odd).
-constexpr int kStripL3Floats = (kFullSlots + 1) * kL3Entries;  // 702 per group
-constexpr int kStripL2Floats = kFullSlots * kL2Entries;        // 225 per group
-static_assert(kStripL3Floats + kStripL2Floats == kLutFloats, "the regions hold every group's 927 floats");
+constexpr int kStripL3Floats = kLut3Floats;  // 702 per group
+constexpr int kStripL2Floats = kLut2Floats;  // 225 per group
 static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows <= kStripLdsFloats, "LDS fits");
 constexpr int kStripTrit3Iters = (kStripMaxGroups * (kFullSlots + 1) + kStripThreads - 1) / kStripThreads;
 constexpr int kStripL2Iters = (kStripMaxGroups * kFullSlots + kStripThreads - 1) / kStripThreads;
