@@ -1249,10 +1249,14 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
             for (int g = (q * G) >> 3; g < g1; ++g) part += v[g * R];
         }
         // DPP: quad_perm [1, 0, 3, 2] swaps neighbours, [2, 3, 0, 1] pairs,
-        // row_shl:4 (0x104) reads the lane four above.
-        const float pair = part + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part), 0xb1, 0xf, 0xf, false));
-        const float quad = pair + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pair), 0x4e, 0xf, 0xf, false));
-        const float total = quad + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(quad), 0x104, 0xf, 0xf, false));
+        // row_shl:4 (0x104) reads the lane four above (lanes 12-15 of a row
+        // of 16, whose sums are not used, read 0).
+        const float pair =
+            part + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0xb1, 0xf, 0xf, false));
+        const float quad =
+            pair + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(pair), 0x4e, 0xf, 0xf, false));
+        const float total =
+            quad + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(quad), 0x104, 0xf, 0xf, false));
         if constexpr (GLU) {
             // Rows 2r and 2r + 1 (lo is even) sit eight lanes apart.
             const T own = from_f32<T>(total);
