@@ -969,10 +969,13 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // strip_gemv_kernel: the M = 1 decode GEMV (one activation vector) for
 // matrices of at most kStripMaxGroups groups per row (K <= 5120) and at most
 // 96 rows per CU, with every row's K reduction inside one workgroup (the
-// LUT23 algorithm of src/ternel_mlx/kernels.py:244-342).
+// LUT23 algorithm of src/ternel_mlx/kernels.py:244-342). With SPLIT, rows of
+// 41 to 80 groups: two workgroups per strip each take one K chunk of at most
+// 40 groups, and the strip's rows are met through fp32 partials (the
+// epilogue below).
 //
-// One workgroup per CU owns a strip of R <= 96 rows: strip s holds rows
-// [2 floor(s U / P), 2 floor((s + 1) U / P)), U = ceil(N / 2), so strips
+// One workgroup per CU owns a strip of R <= 96 rows: strip s of S holds rows
+// [2 floor(s U / S), 2 floor((s + 1) U / S)), U = ceil(N / 2), so strips
 // differ by at most two rows and a gate/up pair never straddles two of them.
 // Workgroup b takes strip (b % 8) P / 8 + b / 8 when P is a multiple of 8:
 // workgroups are dealt to the eight XCDs in turn, so each XCD holds adjacent
@@ -1014,22 +1017,25 @@ constexpr int kStripLdsFloats = 40960;  // 160 KiB, the workgroup limit
 // (27 and 9 are odd).
 constexpr int kStripL3Floats = kLut3Floats;  // 702 per group
 constexpr int kStripL2Floats = kLut2Floats;  // 225 per group
-static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows <= kStripLdsFloats, "LDS fits");
+static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows < kStripLdsFloats,
+              "LDS fits, with the last float free for the split's flag");
 constexpr int kStripTrit3Iters = (kStripMaxGroups * (kFullSlots + 1) + kStripThreads - 1) / kStripThreads;
 constexpr int kStripL2Iters = (kStripMaxGroups * kFullSlots + kStripThreads - 1) / kStripThreads;
 // Below this many rows the LUT23 kernel is used instead (equal speed).
 constexpr int kStripMinRows = 2048;
 
 struct StripGeometry {
-    int N, G;
-    int P;
+    int N, G;        // rows, groups per row
+    int P;           // workgroups: S strips x Z K chunks
+    int S, Z;        // strips; K chunks of at most Gc groups (Z = 1: no split)
+    int Gc;
     int units;       // U = ceil(N / 2)
     int value_base;  // LDS float offset of the block values (and, before them, the staged activations)
 };
 
 // First row of strip s.
 __device__ __forceinline__ int strip_row(int s, const StripGeometry &geo) {
-    return min(geo.N, 2 * static_cast<int>(static_cast<unsigned>(s * geo.units) / static_cast<unsigned>(geo.P)));
+    return min(geo.N, 2 * static_cast<int>(static_cast<unsigned>(s * geo.units) / static_cast<unsigned>(geo.S)));
 }
 
 // The table tasks of one thread: three-trit task t < 26 G is (group t / 26,
@@ -1121,21 +1127,33 @@ __device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords
 // STAGE: the activations are a 2-byte type at a 16-byte aligned address and
 // are staged in LDS with one 16-byte load per thread; otherwise each thread
 // reads its table tasks' activations from global memory.
-template <typename T, bool GLU, bool STAGE, int PAIRS>
+template <typename T, bool GLU, bool STAGE, int PAIRS, bool SPLIT>
 __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint32_t *__restrict__ packed,
                                                                       const T *__restrict__ x, T *__restrict__ y,
+                                                                      float *__restrict__ partial,
+                                                                      unsigned *__restrict__ counters,
                                                                       StripGeometry geo) {
+    static_assert(!(SPLIT && GLU), "the fused SwiGLU form is not split");
     __shared__ __align__(16) float lds_f[kStripLdsFloats];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.x;
-    const int G = geo.G;
     const int strip_wave_id = b * kStripWaves + wave;
     (void)strip_wave_id;
     TQ1_PHASE(strip_wave_id, 0);
     TQ1_PHASE_XCC(strip_wave_id);
+
+    // Workgroup order: b takes (b % 8) P / 8 + b / 8 where P is a multiple of
+    // 8, so each XCD holds a contiguous run; that index is strip u / Z, K
+    // chunk u % Z (a strip's chunks run on one XCD).
+    const int u = (geo.P & 7) == 0 ? (b & 7) * (geo.P >> 3) + (b >> 3) : b;
+    const int s = SPLIT ? u / geo.Z : u;
+    const int z = SPLIT ? u - s * geo.Z : 0;
+    const int g_lo = z * geo.Gc;                           // first group of this chunk
+    const int G = SPLIT ? min(geo.Gc, geo.G - g_lo) : geo.G;  // this workgroup's groups
+    x += static_cast<int64_t>(g_lo) * kBlockWeights;
 
     // Activations first.
     constexpr int kVec = 16 / static_cast<int>(sizeof(T));
@@ -1148,7 +1166,6 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
     else
         tasks.gather(x, G, tid);
 
-    const int s = (geo.P & 7) == 0 ? (b & 7) * (geo.P >> 3) + (b >> 3) : b;
     const int lo = strip_row(s, geo);
     const int R = strip_row(s + 1, geo) - lo;
     const int RG = R * G;
@@ -1169,8 +1186,9 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
         g = static_cast<int>((static_cast<float>(tc) + 0.5f) * inv_r);
         // (Every factor and result here is below 2^24.)
         const uint32_t row = static_cast<uint32_t>(lo + tc) - mul_u24(static_cast<uint32_t>(g), static_cast<uint32_t>(R));
-        return static_cast<int>(mad_u24(mad_u24(row >> 6, static_cast<uint32_t>(G), static_cast<uint32_t>(g)),
-                                        static_cast<uint32_t>(kTileGroupWords), row & 63u));
+        return static_cast<int>(
+            mad_u24(mad_u24(row >> 6, static_cast<uint32_t>(geo.G), static_cast<uint32_t>(g_lo + g)),
+                    static_cast<uint32_t>(kTileGroupWords), row & 63u));
     };
     // (The scheduling barriers keep the sums of the item before from moving
     // above the loads, where they would wait for that item's words first.)
@@ -1262,8 +1280,35 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
             const T own = from_f32<T>(total);
             const float partner = __shfl_xor(to_f32<T>(own), 8, 64);
             if (i < R && (tid & 15) == 0) y[(lo + i) / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
+        } else if constexpr (SPLIT) {
+            if (i < R && q == 0)
+                __hip_atomic_store(partial + static_cast<int64_t>(z) * geo.N + lo + i, total, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         } else {
             if (i < R && q == 0) y[lo + i] = from_f32<T>(total);
+        }
+    }
+    if constexpr (SPLIT) {
+        // The K chunks of a strip meet as the (tile, group) kernel's split-K
+        // chunks do: each publishes its rows' partial sums with agent-scope
+        // (sc1) stores, waits until they are acknowledged at the device's
+        // coherence point, and counts itself in with a relaxed agent-scope
+        // atomic; the workgroup that brings the strip's count to Z reads the
+        // Z partials of each row with agent-scope loads, adds them in chunk
+        // order and re-arms the counter. The flag lives in the LDS float the
+        // values never reach.
+        unsigned *const s_last = reinterpret_cast<unsigned *>(lds_f) + (kStripLdsFloats - 1);
+        asm volatile("" ::: "memory");
+        wait_vector_memory();
+        asm volatile("" ::: "memory");
+        __syncthreads();
+        if (tid == 0)
+            *s_last = __hip_atomic_fetch_add(counters + s, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      static_cast<unsigned>(geo.Z - 1);
+        __syncthreads();
+        if (*s_last) {
+            if (tid < R) y[lo + tid] = from_f32<T>(sum_partials_in_order(partial + lo + tid, geo.N, geo.Z));
+            if (tid == 0) __hip_atomic_store(counters + s, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     TQ1_PHASE(strip_wave_id, 4);  // done
@@ -3068,45 +3113,77 @@ int launch_lut_once(const uint32_t *packed, const void *x, void *y, int64_t M, i
 }
 
 // The M = 1 strip GEMV (strip_gemv_kernel): one workgroup per CU, at most
-// one per two rows, for strips of at most 96 rows and at most 40 groups.
-int plan_strip(int64_t rows, int64_t columns, StripGeometry *geo) {
+// one per two rows, for strips of at most 96 rows. Rows of 41 to 80 groups
+// (with allow_split) are cut into Z = 2 K chunks, one workgroup per (strip,
+// chunk), S = CUs / 2 strips, met by the split-K hand-off in a workspace
+// (strip_workspace_bytes). (Measured on MI355X against the (tile, group)
+// kernel: O 8192 -> 5120 7.9 against 8.3 us, 6144 -> 5120 7.3 against 7.4;
+// four chunks of down's 136 groups 11.1-11.4 against 10.2, the hand-off
+// outweighing the shorter chain.)
+constexpr int kStripMaxChunks = 2;
+int plan_strip(int64_t rows, int64_t columns, StripGeometry *geo, bool allow_split = true) {
     const int64_t G = columns / kBlockWeights;
-    if (G > kStripMaxGroups) return fail(TERNEL_TQ1_EINVAL, "the strip GEMV takes at most %d groups per row", kStripMaxGroups);
+    int64_t Z = 1;
+    if (G > kStripMaxGroups) {
+        Z = ceil_div(G, kStripMaxGroups);
+        if (!allow_split || Z > kStripMaxChunks)
+            return fail(TERNEL_TQ1_EINVAL, "the strip GEMV takes at most %d groups per row%s",
+                        allow_split ? kStripMaxChunks * kStripMaxGroups : kStripMaxGroups,
+                        allow_split ? " (in K chunks of at most 40)" : " here");
+    }
+    const int64_t Gc = ceil_div(G, Z);
     const int64_t units = (rows + 1) / 2;
-    const int64_t P = std::max<int64_t>(1, std::min<int64_t>(device_cu_count(), units));
-    if (2 * ceil_div(units, P) > kStripMaxRows)
+    const int64_t S = std::max<int64_t>(1, std::min<int64_t>(device_cu_count() / Z, units));
+    if (2 * ceil_div(units, S) > kStripMaxRows)
         return fail(TERNEL_TQ1_EINVAL, "strips of %lld rows are past the strip GEMV's %d",
-                    static_cast<long long>(2 * ceil_div(units, P)), kStripMaxRows);
-    if (P * units > INT32_MAX || rows * G * kBlockWords > INT32_MAX)
+                    static_cast<long long>(2 * ceil_div(units, S)), kStripMaxRows);
+    if (S * units > INT32_MAX || rows * G * kBlockWords > INT32_MAX || Z * rows > INT32_MAX)
         return fail(TERNEL_TQ1_EINVAL, "tensor too large for the strip GEMV's 32-bit indices");
+    if (S > kUsableCounters) return fail(TERNEL_TQ1_EINVAL, "more strips than the counter region holds");
     geo->N = static_cast<int>(rows);
     geo->G = static_cast<int>(G);
-    geo->P = static_cast<int>(P);
+    geo->S = static_cast<int>(S);
+    geo->Z = static_cast<int>(Z);
+    geo->Gc = static_cast<int>(Gc);
+    geo->P = static_cast<int>(S * Z);
     geo->units = static_cast<int>(units);
-    geo->value_base = static_cast<int>((G * kLutFloats + 3) / 4 * 4);
+    geo->value_base = static_cast<int>((Gc * kLutFloats + 3) / 4 * 4);
     return TERNEL_TQ1_OK;
+}
+
+// The split strip GEMV's workspace: the counter region, then Z x N fp32
+// partials (0 without a split).
+size_t strip_workspace_bytes(const StripGeometry &geo) {
+    return geo.Z > 1 ? kPartialOffset + static_cast<size_t>(geo.Z) * geo.N * sizeof(float) : 0;
 }
 
 template <typename T>
 int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeometry &geo, hipStream_t stream,
-                 bool glu) {
+                 bool glu, void *ws = nullptr) {
     const dim3 grid(static_cast<unsigned>(geo.P));
     const bool stage = sizeof(T) == 2 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    const bool split = geo.Z > 1;
+    if (split && (glu || !ws)) return fail(TERNEL_TQ1_EINVAL, "a split strip GEMV needs a workspace and no SwiGLU");
     const T *xt = static_cast<const T *>(x);
     T *yt = static_cast<T *>(y);
-    // Items per wave: the largest strip's ceil(R G / 64) items over 16 waves.
-    const int64_t max_rows = 2 * ((geo.units + geo.P - 1) / geo.P);
-    const int64_t per_wave = ceil_div(ceil_div(max_rows * geo.G, 64), kStripWaves);
+    unsigned *counters = split ? static_cast<unsigned *>(ws) : nullptr;
+    float *partial = split ? reinterpret_cast<float *>(static_cast<char *>(ws) + kPartialOffset) : nullptr;
+    // Items per wave: the largest strip's ceil(R Gc / 64) items over 16 waves.
+    const int64_t max_rows = 2 * ((geo.units + geo.S - 1) / geo.S);
+    const int64_t per_wave = ceil_div(ceil_div(max_rows * geo.Gc, 64), kStripWaves);
     if (per_wave > 4) return fail(TERNEL_TQ1_EINVAL, "strip of %lld items per wave", static_cast<long long>(per_wave));
     const bool two_pairs = per_wave > 2;
 #define TQ1_STRIP_LAUNCH_P(STAGE, PAIRS)                                                                        \
     do {                                                                                                        \
         if (glu)                                                                                                \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE, PAIRS>), grid, dim3(kStripThreads), 0, stream, \
-                               packed, xt, yt, geo);                                                           \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE, PAIRS, false>), grid, dim3(kStripThreads), 0,  \
+                               stream, packed, xt, yt, partial, counters, geo);                                \
+        else if (split)                                                                                         \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, PAIRS, true>), grid, dim3(kStripThreads), 0,  \
+                               stream, packed, xt, yt, partial, counters, geo);                                \
         else                                                                                                    \
-            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, PAIRS>), grid, dim3(kStripThreads), 0, stream,\
-                               packed, xt, yt, geo);                                                           \
+            hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, PAIRS, false>), grid, dim3(kStripThreads), 0, \
+                               stream, packed, xt, yt, partial, counters, geo);                                \
     } while (0)
 #define TQ1_STRIP_LAUNCH(STAGE)               \
     do {                                      \
@@ -3130,12 +3207,13 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
 }
 
 // The automatic configuration of one activation vector runs the strip GEMV
-// where it applies (the LUT23 kernel above otherwise).
-bool uses_strip_gemv(int64_t M, int batch_tile, int k_split, int64_t rows, int64_t columns) {
+// where it applies (the LUT23 kernel above otherwise); allow_split admits
+// rows of more than 40 groups (not for the fused SwiGLU form).
+bool uses_strip_gemv(int64_t M, int batch_tile, int k_split, int64_t rows, int64_t columns, bool allow_split = true) {
     if (M != 1 || batch_tile != 0 || k_split != 0 || rows < kStripMinRows) return false;
     StripGeometry geo;
     const std::string saved = g_last_error;
-    const bool ok = plan_strip(rows, columns, &geo) == TERNEL_TQ1_OK;
+    const bool ok = plan_strip(rows, columns, &geo, allow_split) == TERNEL_TQ1_OK;
     snprintf(g_last_error, sizeof(g_last_error), "%s", saved.c_str());
     return ok;
 }
@@ -3769,7 +3847,10 @@ int ternel_tq1_deinterleave(const uint32_t *packed, int64_t rows, int64_t column
 
 size_t ternel_tq1_matmul_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int batch_tile, int k_split) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK) return 0;
-    if (uses_strip_gemv(M, batch_tile, k_split, rows, columns)) return 0;
+    if (uses_strip_gemv(M, batch_tile, k_split, rows, columns)) {
+        StripGeometry geo;
+        return plan_strip(rows, columns, &geo) == TERNEL_TQ1_OK ? strip_workspace_bytes(geo) : 0;
+    }
     LutPlan plan;
     if (plan_lut(M, rows, columns, batch_tile, k_split, &plan) != TERNEL_TQ1_OK) return 0;
     return plan.counter_bytes + plan.partial_bytes;
@@ -3786,14 +3867,18 @@ int ternel_tq1_matmul(const uint32_t *packed, const void *x, void *y, int64_t M,
         if ((rc = plan_strip(rows, columns, &geo)) != TERNEL_TQ1_OK) return rc;
         if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
         if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
+        const size_t need = strip_workspace_bytes(geo);
+        if (need && (!ws || ws_bytes < need))
+            return fail(TERNEL_TQ1_EINVAL, "workspace of %zu bytes is smaller than the %zu the split needs", ws_bytes,
+                        need);
         hipStream_t s = static_cast<hipStream_t>(stream);
         switch (dtype) {
             case TERNEL_TQ1_F16:
-                return launch_strip<_Float16>(packed, x, y, geo, s, false);
+                return launch_strip<_Float16>(packed, x, y, geo, s, false, ws);
             case TERNEL_TQ1_BF16:
-                return launch_strip<bf16_t>(packed, x, y, geo, s, false);
+                return launch_strip<bf16_t>(packed, x, y, geo, s, false, ws);
             default:
-                return launch_strip<float>(packed, x, y, geo, s, false);
+                return launch_strip<float>(packed, x, y, geo, s, false, ws);
         }
     }
     LutPlan plan;
@@ -3822,19 +3907,28 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
     if ((rc = check_geometry(M, rows, columns)) != TERNEL_TQ1_OK) return rc;
     if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
     if (uses_strip_gemv(M, batch_tile, k_split, rows, columns)) {
-        // the same kernel as ternel_tq1_matmul, which takes no workspace
+        // the same kernel as ternel_tq1_matmul; a split one meets its K
+        // chunks in the static scratch
         StripGeometry geo;
         if ((rc = plan_strip(rows, columns, &geo)) != TERNEL_TQ1_OK) return rc;
         if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
         if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
+        void *ws = nullptr;
+        if (geo.Z > 1) {
+            if (strip_workspace_bytes(geo) - kPartialOffset > static_cast<size_t>(kNoAllocPartialBytes))
+                return fail(TERNEL_TQ1_EINVAL, "a split strip GEMV of %lld rows needs more partials than the %lld "
+                            "bytes of the static scratch", static_cast<long long>(rows),
+                            static_cast<long long>(kNoAllocPartialBytes));
+            if ((rc = noalloc_scratch(s, &ws)) != TERNEL_TQ1_OK) return rc;
+        }
         switch (dtype) {
             case TERNEL_TQ1_F16:
-                return launch_strip<_Float16>(packed, x, y, geo, s, false);
+                return launch_strip<_Float16>(packed, x, y, geo, s, false, ws);
             case TERNEL_TQ1_BF16:
-                return launch_strip<bf16_t>(packed, x, y, geo, s, false);
+                return launch_strip<bf16_t>(packed, x, y, geo, s, false, ws);
             default:
-                return launch_strip<float>(packed, x, y, geo, s, false);
+                return launch_strip<float>(packed, x, y, geo, s, false, ws);
         }
     }
     LutPlan plan;
@@ -3988,7 +4082,8 @@ int ternel_tq1_linear_kernel(int64_t M, int64_t rows, int64_t columns, int dtype
 size_t ternel_tq1_swiglu_workspace_bytes(int64_t M, int64_t rows, int64_t columns, int dtype) {
     if (check_geometry(M, rows, columns) != TERNEL_TQ1_OK || rows % 2) return 0;
     if (linear_uses_lut(M, rows, columns, dtype))
-        return ternel_tq1_matmul_workspace_bytes(M, rows, columns, uses_strip_gemv(M, 0, 0, rows, columns) ? 0 : 1, 0);
+        return ternel_tq1_matmul_workspace_bytes(M, rows, columns, uses_strip_gemv(M, 0, 0, rows, columns, false) ? 0 : 1,
+                                                 0);
     return swiglu_pairs_offset(M, rows, columns, dtype) + static_cast<size_t>(M) * rows * sizeof(_Float16);
 }
 
@@ -4004,9 +4099,9 @@ int ternel_tq1_swiglu(const uint32_t *packed, const void *x, void *z, int64_t M,
     if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
     if (!x || !z) return fail(TERNEL_TQ1_EINVAL, "null pointer");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (linear_uses_lut(M, rows, columns, dtype) && uses_strip_gemv(M, 0, 0, rows, columns)) {
+    if (linear_uses_lut(M, rows, columns, dtype) && uses_strip_gemv(M, 0, 0, rows, columns, false)) {
         StripGeometry geo;
-        if ((rc = plan_strip(rows, columns, &geo)) != TERNEL_TQ1_OK) return rc;
+        if ((rc = plan_strip(rows, columns, &geo, false)) != TERNEL_TQ1_OK) return rc;
         switch (dtype) {
             case TERNEL_TQ1_F16:
                 return launch_strip<_Float16>(packed, x, z, geo, s, true);

@@ -277,10 +277,13 @@ def test_auto_split_gemv_carries_non_finite_activations_to_every_row(bad: float,
 def test_a_vector_sums_the_same_in_any_batch_and_workgroup_shape(rows: int, columns: int) -> None:
     """At M=1 these splits run 128-row workgroups (down: 340 of 256 rows would
     leave most CUs one and some two), at M=2 256-row ones: each row's chunk
-    and block order is the same, so the first vector's outputs are identical."""
+    and block order is the same, so the first vector's outputs are identical.
+    (batch_tile=1 keeps M=1 on this kernel: left automatic, one vector over
+    more than 40 groups takes the split strip GEMV.)"""
     blocks = random_blocks(rows, columns, seed=rows + columns)
     x = np.random.default_rng(columns).normal(0.0, 1.0, size=(2, columns)).astype(np.float32)
-    one = run_auto(blocks, x[:1]).cpu().numpy()
+    one = tq1_matmul_words(pack(blocks), to_dev(x[:1]), layout=layout(rows, columns),
+                           config=MatmulConfig(batch_tile=1)).cpu().numpy()
     two = run_auto(blocks, x).cpu().numpy()
     np.testing.assert_array_equal(two[:1], one)
     oracle = O.oracle_matmul(blocks, x[:1], rows=rows, columns=columns)

@@ -132,3 +132,81 @@ def test_fused_swiglu_form(dtype, rows) -> None:
     g64, u64 = oracle[:, 0::2], oracle[:, 1::2]
     ref = g64 / (1.0 + np.exp(-g64)) * u64
     assert O.compare(got.cpu().numpy(), ref)["normalised_max_abs_error"] < 4 * TOLERANCE[dtype]
+
+
+# --- rows of 41 to 80 groups: the strip GEMV in Z = 2 K chunks, one workgroup
+# per (strip, chunk), S = CUs / 2 strips, met through two fp32 partials per
+# row added in chunk order by the chunk that arrives last.
+
+COUNTERS = 64 * 1024  # the workspace's counter region
+
+
+def takes_split_strip(rows: int, columns: int, chunks: int) -> bool:
+    return _lib.lib().ternel_tq1_matmul_workspace_bytes(1, rows, columns, 0, 0) == COUNTERS + chunks * rows * 4
+
+
+def run_split(blocks: np.ndarray, x: torch.Tensor, chunks: int) -> torch.Tensor:
+    rows, g, _ = blocks.shape
+    assert takes_split_strip(rows, g * 128, chunks), f"{rows}x{g * 128} does not take the split strip GEMV"
+    out = tq1_matmul_words(pack(blocks), x, layout=layout(rows, g * 128), config=MatmulConfig())
+    torch.cuda.synchronize()
+    return out
+
+
+# (rows, columns, chunks): O 8192 -> 5120 (2 x 32 groups, 40-row strips);
+# out_proj 6144 -> 5120 (2 x 24); 41 groups (chunks of 21 and 20) over an odd
+# row count; 80 groups (2 x 40) over 18-row and over 64-row strips (three
+# items per wave).
+SPLIT_SHAPES = ((5120, 8192, 2), (5120, 6144, 2), (3001, 5248, 2), (2050, 10240, 2), (8192, 10240, 2))
+
+
+@pytest.mark.parametrize(("rows", "columns", "chunks"), SPLIT_SHAPES)
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+def test_split_strip_gemv_matches_the_oracle(rows, columns, chunks, dtype) -> None:
+    print(f"split strip: rows={rows} columns={columns} chunks={chunks} {dtype}", flush=True)
+    blocks = random_blocks(rows, columns, seed=rows * 5 + columns)
+    x = np.random.default_rng(rows + 3 * columns).normal(0.0, 1.0, size=(1, columns)).astype(np.float32)
+    xd = to_dev(x).to(dtype)
+    got = run_split(blocks, xd, chunks).float().cpu().numpy()
+    oracle = O.oracle_matmul(blocks, xd.float().cpu().numpy().astype(np.float64), rows=rows, columns=columns)
+    assert O.compare(got, oracle)["normalised_max_abs_error"] < TOLERANCE[dtype]
+
+
+def test_split_strip_gemv_is_exact_on_integer_data() -> None:
+    """Unit scales and +/-1 activations: every block sum, chunk partial and
+    total is an exact integer, whatever the order."""
+    rows, columns = 5120, 10240
+    groups = columns // 128
+    rng = np.random.default_rng(41)
+    scales = np.full(rows * groups, 1.0, dtype=np.float16).view(np.uint8).reshape(-1, 2)
+    trits = rng.integers(0, 3, size=(rows * groups, 128), dtype=np.uint8)
+    blocks = O.encode_tq1_blocks(scales, trits).reshape(rows, groups, 28)
+    x = rng.choice((-1.0, 1.0), size=(1, columns)).astype(np.float32)
+    got = run_split(blocks, to_dev(x), 2).cpu().numpy()
+    np.testing.assert_array_equal(got, O.oracle_matmul(blocks, x, rows=rows, columns=columns))
+
+
+def test_split_strip_gemv_rearms_its_counters_and_repeats_bit_for_bit() -> None:
+    """Back-to-back calls of two shapes (different strip counts) on the
+    library's workspace: each call finds its counters at zero and leaves them
+    there, so every repeat is bit-identical."""
+    a = random_blocks(8192, 10240, seed=3)
+    b = random_blocks(5120, 8192, seed=4)
+    xa = to_dev(np.random.default_rng(3).normal(0.0, 1.0, size=(1, 10240)).astype(np.float16))
+    xb = to_dev(np.random.default_rng(4).normal(0.0, 1.0, size=(1, 8192)).astype(np.float16))
+    first_a = run_split(a, xa, 2).view(torch.int16).clone()
+    first_b = run_split(b, xb, 2).view(torch.int16).clone()
+    for _ in range(3):
+        assert torch.equal(run_split(a, xa, 2).view(torch.int16), first_a)
+        assert torch.equal(run_split(b, xb, 2).view(torch.int16), first_b)
+
+
+def test_split_strip_gemv_unaligned_activations_give_the_same_result() -> None:
+    rows, columns = 5120, 8192
+    blocks = random_blocks(rows, columns, seed=23)
+    x = np.random.default_rng(23).normal(0.0, 1.0, size=(1, columns)).astype(np.float16)
+    storage = torch.zeros(columns + 8, dtype=torch.float16, device="cuda")
+    view = storage[5:5 + columns].view(1, columns)
+    view.copy_(to_dev(x))
+    assert view.data_ptr() % 16 != 0
+    assert torch.equal(run_split(blocks, view, 2).view(torch.int16), run_split(blocks, to_dev(x), 2).view(torch.int16))
