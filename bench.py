@@ -50,6 +50,19 @@ def ring_copies(matrix_bytes: int) -> int:
     return max(RING_COPIES_MIN, -(-RING_BYTES_MIN // matrix_bytes))
 
 
+def m1_form(handle, rows: int, columns: int) -> str:
+    """The M=1 form the automatic configuration runs, read from its workspace
+    query: none for the strip GEMV, the 64 KiB counter region plus two fp32
+    partials per row for its two-K-chunk form (from 2048 rows), anything else
+    for the (tile, group) LUT23 kernel."""
+    ws = handle.ternel_tq1_matmul_workspace_bytes(1, rows, columns, 0, 0)
+    if rows >= 2048 and ws == 0:
+        return "strip"
+    if rows >= 2048 and ws == 64 * 1024 + 2 * rows * 4:
+        return "strip, two K chunks"
+    return "lut23"
+
+
 def packed_bytes(K: int, N: int) -> int:
     return N * (K // 128) * 28
 
@@ -901,8 +914,7 @@ def census_stream(torch, synthetic, pack_weights, PackedTensorLayout, graph_of, 
         del g
         nbytes = packed_bytes(columns, rows)
         shapes[key] = {"tensor": name, "per_token": len(idx), "distinct_copies": len(idx), "us": round(us, 3),
-                       "GB/s": round(nbytes / us / 1e3, 1), "kernel": "strip" if handle.ternel_tq1_matmul_workspace_bytes(
-                           1, rows, columns, 0, 0) == 0 else "lut23"}
+                       "GB/s": round(nbytes / us / 1e3, 1), "kernel": m1_form(handle, rows, columns)}
     del weights, bufs
     return {
         "workload": "the reference's 497-tensor model-order traversal (27B census, src/ternel_mlx/layout.py:179-195): "
