@@ -52,14 +52,14 @@ def ring_copies(matrix_bytes: int) -> int:
 
 def m1_form(handle, rows: int, columns: int) -> str:
     """The M=1 form the automatic configuration runs, read from its workspace
-    query: none for the strip GEMV, the 64 KiB counter region plus two fp32
-    partials per row for its two-K-chunk form (from 2048 rows), anything else
-    for the (tile, group) LUT23 kernel."""
+    query (from 2048 rows): none for the strip GEMV, the 64 KiB counter region
+    alone for its K-chunk form, counters and partials for the (tile, group)
+    LUT23 kernel."""
     ws = handle.ternel_tq1_matmul_workspace_bytes(1, rows, columns, 0, 0)
     if rows >= 2048 and ws == 0:
         return "strip"
-    if rows >= 2048 and ws == 64 * 1024 + 2 * rows * 4:
-        return "strip, two K chunks"
+    if rows >= 2048 and ws == 64 * 1024:
+        return f"strip, {-(-columns // 128 // 40)} K chunks"
     return "lut23"
 
 

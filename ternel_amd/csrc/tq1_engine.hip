@@ -970,8 +970,8 @@ __global__ __launch_bounds__(RT * kTileRows * KW) void lut_gemv_kernel(
 // matrices of at most kStripMaxGroups groups per row (K <= 5120) and at most
 // 96 rows per CU, with every row's K reduction inside one workgroup (the
 // LUT23 algorithm of src/ternel_mlx/kernels.py:244-342). With SPLIT, rows of
-// 41 to 80 groups: two workgroups per strip each take one K chunk of at most
-// 40 groups, and the strip's rows are met through fp32 partials (the
+// more than 40 groups: Z <= 4 workgroups per strip each take one K chunk of
+// at most 40 groups, and each row's Z partials meet in exchange slots (the
 // epilogue below).
 //
 // One workgroup per CU owns a strip of R <= 96 rows: strip s of S holds rows
@@ -1017,8 +1017,7 @@ constexpr int kStripLdsFloats = 40960;  // 160 KiB, the workgroup limit
 // (27 and 9 are odd).
 constexpr int kStripL3Floats = kLut3Floats;  // 702 per group
 constexpr int kStripL2Floats = kLut2Floats;  // 225 per group
-static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows < kStripLdsFloats,
-              "LDS fits, with the last float free for the split's flag");
+static_assert(kStripMaxGroups * kLutFloats + kStripMaxGroups * kStripMaxRows <= kStripLdsFloats, "LDS fits");
 constexpr int kStripTrit3Iters = (kStripMaxGroups * (kFullSlots + 1) + kStripThreads - 1) / kStripThreads;
 constexpr int kStripL2Iters = (kStripMaxGroups * kFullSlots + kStripThreads - 1) / kStripThreads;
 // Below this many rows the LUT23 kernel is used instead (equal speed).
@@ -1130,8 +1129,7 @@ __device__ __forceinline__ float strip_block_sum(const uint32_t (&w)[kBlockWords
 template <typename T, bool GLU, bool STAGE, int PAIRS, bool SPLIT>
 __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint32_t *__restrict__ packed,
                                                                       const T *__restrict__ x, T *__restrict__ y,
-                                                                      float *__restrict__ partial,
-                                                                      unsigned *__restrict__ counters,
+                                                                      unsigned *__restrict__ slots,
                                                                       StripGeometry geo) {
     static_assert(!(SPLIT && GLU), "the fused SwiGLU form is not split");
     __shared__ __align__(16) float lds_f[kStripLdsFloats];
@@ -1281,34 +1279,43 @@ __global__ __launch_bounds__(kStripThreads, 1) void strip_gemv_kernel(const uint
             const float partner = __shfl_xor(to_f32<T>(own), 8, 64);
             if (i < R && (tid & 15) == 0) y[(lo + i) / 2] = swiglu_pair<T>(own, from_f32<T>(partner));
         } else if constexpr (SPLIT) {
-            if (i < R && q == 0)
-                __hip_atomic_store(partial + static_cast<int64_t>(z) * geo.N + lo + i, total, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            // The Z chunks of a row meet in a fixed binary tree of exchange
+            // slots: Z = 2 (c0 + c1), 3 ((c0 + c1) + c2), 4 ((c0 + c1) +
+            // (c2 + c3)). At each node a chunk swaps its value into the slot
+            // (an agent-scope atomic exchange): finding the slot empty it
+            // leaves; finding its sibling's value it adds the two, left child
+            // first (two operands: the same sum whichever arrives first),
+            // empties the slot and goes on up. The chunk that completes the
+            // root stores the row. One atomic round trip per level, nothing to
+            // wait for, and the slots are empty again after every call.
+            if (i < R && q == 0) {
+                unsigned *const row_slots = slots + lo + i;
+                const int N = geo.N;
+                float v = total;
+                auto merge = [&](int node, bool right) __attribute__((always_inline)) {
+                    // 0 is an empty slot: values travel as their bits + 1,
+                    // NaNs as the quiet NaN (whose bits + 1 is not 0).
+                    const uint32_t bits = v != v ? 0x7fc00000u : __float_as_uint(v);
+                    const unsigned old = __hip_atomic_exchange(row_slots + static_cast<int64_t>(node) * N, bits + 1u,
+                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (old == 0u) return false;
+                    const float other = __uint_as_float(old - 1u);
+                    v = right ? other + v : v + other;
+                    __hip_atomic_store(row_slots + static_cast<int64_t>(node) * N, 0u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    return true;
+                };
+                bool root;
+                if (geo.Z == 2)
+                    root = merge(0, z == 1);
+                else if (geo.Z == 3)
+                    root = (z == 2 || merge(0, z == 1)) && merge(1, z == 2);
+                else
+                    root = merge(z >> 1, (z & 1) != 0) && merge(2, z >= 2);
+                if (root) y[lo + i] = from_f32<T>(v);
+            }
         } else {
             if (i < R && q == 0) y[lo + i] = from_f32<T>(total);
-        }
-    }
-    if constexpr (SPLIT) {
-        // The K chunks of a strip meet as the (tile, group) kernel's split-K
-        // chunks do: each publishes its rows' partial sums with agent-scope
-        // (sc1) stores, waits until they are acknowledged at the device's
-        // coherence point, and counts itself in with a relaxed agent-scope
-        // atomic; the workgroup that brings the strip's count to Z reads the
-        // Z partials of each row with agent-scope loads, adds them in chunk
-        // order and re-arms the counter. The flag lives in the LDS float the
-        // values never reach.
-        unsigned *const s_last = reinterpret_cast<unsigned *>(lds_f) + (kStripLdsFloats - 1);
-        asm volatile("" ::: "memory");
-        wait_vector_memory();
-        asm volatile("" ::: "memory");
-        __syncthreads();
-        if (tid == 0)
-            *s_last = __hip_atomic_fetch_add(counters + s, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                      static_cast<unsigned>(geo.Z - 1);
-        __syncthreads();
-        if (*s_last) {
-            if (tid < R) y[lo + tid] = from_f32<T>(sum_partials_in_order(partial + lo + tid, geo.N, geo.Z));
-            if (tid == 0) __hip_atomic_store(counters + s, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     TQ1_PHASE(strip_wave_id, 4);  // done
@@ -3113,14 +3120,12 @@ int launch_lut_once(const uint32_t *packed, const void *x, void *y, int64_t M, i
 }
 
 // The M = 1 strip GEMV (strip_gemv_kernel): one workgroup per CU, at most
-// one per two rows, for strips of at most 96 rows. Rows of 41 to 80 groups
-// (with allow_split) are cut into Z = 2 K chunks, one workgroup per (strip,
-// chunk), S = CUs / 2 strips, met by the split-K hand-off in a workspace
-// (strip_workspace_bytes). (Measured on MI355X against the (tile, group)
-// kernel: O 8192 -> 5120 7.9 against 8.3 us, 6144 -> 5120 7.3 against 7.4;
-// four chunks of down's 136 groups 11.1-11.4 against 10.2, the hand-off
-// outweighing the shorter chain.)
-constexpr int kStripMaxChunks = 2;
+// one per two rows, for strips of at most 96 rows. Rows of more than 40
+// groups (with allow_split) are cut into Z <= 4 K chunks of at most 40 groups,
+// one workgroup per (strip, chunk), S = CUs / Z strips, whose row partials
+// meet in Z - 1 exchange slots per row in the workspace's counter region
+// (strip_workspace_bytes).
+constexpr int kStripMaxChunks = 4;
 int plan_strip(int64_t rows, int64_t columns, StripGeometry *geo, bool allow_split = true) {
     const int64_t G = columns / kBlockWeights;
     int64_t Z = 1;
@@ -3139,7 +3144,9 @@ int plan_strip(int64_t rows, int64_t columns, StripGeometry *geo, bool allow_spl
                     static_cast<long long>(2 * ceil_div(units, S)), kStripMaxRows);
     if (S * units > INT32_MAX || rows * G * kBlockWords > INT32_MAX || Z * rows > INT32_MAX)
         return fail(TERNEL_TQ1_EINVAL, "tensor too large for the strip GEMV's 32-bit indices");
-    if (S > kUsableCounters) return fail(TERNEL_TQ1_EINVAL, "more strips than the counter region holds");
+    if ((Z - 1) * rows > kUsableCounters)
+        return fail(TERNEL_TQ1_EINVAL, "%lld rows in %lld K chunks need more exchange slots than the counter region holds",
+                    static_cast<long long>(rows), static_cast<long long>(Z));
     geo->N = static_cast<int>(rows);
     geo->G = static_cast<int>(G);
     geo->S = static_cast<int>(S);
@@ -3151,11 +3158,9 @@ int plan_strip(int64_t rows, int64_t columns, StripGeometry *geo, bool allow_spl
     return TERNEL_TQ1_OK;
 }
 
-// The split strip GEMV's workspace: the counter region, then Z x N fp32
-// partials (0 without a split).
-size_t strip_workspace_bytes(const StripGeometry &geo) {
-    return geo.Z > 1 ? kPartialOffset + static_cast<size_t>(geo.Z) * geo.N * sizeof(float) : 0;
-}
+// The split strip GEMV's workspace: the counter region, which holds its
+// (Z - 1) N exchange slots (0 without a split).
+size_t strip_workspace_bytes(const StripGeometry &geo) { return geo.Z > 1 ? kCounterRegionBytes : 0; }
 
 template <typename T>
 int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeometry &geo, hipStream_t stream,
@@ -3166,8 +3171,7 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     if (split && (glu || !ws)) return fail(TERNEL_TQ1_EINVAL, "a split strip GEMV needs a workspace and no SwiGLU");
     const T *xt = static_cast<const T *>(x);
     T *yt = static_cast<T *>(y);
-    unsigned *counters = split ? static_cast<unsigned *>(ws) : nullptr;
-    float *partial = split ? reinterpret_cast<float *>(static_cast<char *>(ws) + kPartialOffset) : nullptr;
+    unsigned *slots = split ? static_cast<unsigned *>(ws) : nullptr;
     // Items per wave: the largest strip's ceil(R Gc / 64) items over 16 waves.
     const int64_t max_rows = 2 * ((geo.units + geo.S - 1) / geo.S);
     const int64_t per_wave = ceil_div(ceil_div(max_rows * geo.Gc, 64), kStripWaves);
@@ -3177,13 +3181,13 @@ int launch_strip(const uint32_t *packed, const void *x, void *y, const StripGeom
     do {                                                                                                        \
         if (glu)                                                                                                \
             hipLaunchKernelGGL((strip_gemv_kernel<T, true, STAGE, PAIRS, false>), grid, dim3(kStripThreads), 0,  \
-                               stream, packed, xt, yt, partial, counters, geo);                                \
+                               stream, packed, xt, yt, slots, geo);                                \
         else if (split)                                                                                         \
             hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, PAIRS, true>), grid, dim3(kStripThreads), 0,  \
-                               stream, packed, xt, yt, partial, counters, geo);                                \
+                               stream, packed, xt, yt, slots, geo);                                \
         else                                                                                                    \
             hipLaunchKernelGGL((strip_gemv_kernel<T, false, STAGE, PAIRS, false>), grid, dim3(kStripThreads), 0, \
-                               stream, packed, xt, yt, partial, counters, geo);                                \
+                               stream, packed, xt, yt, slots, geo);                                \
     } while (0)
 #define TQ1_STRIP_LAUNCH(STAGE)               \
     do {                                      \
@@ -3908,20 +3912,14 @@ int ternel_tq1_matmul_noalloc(const uint32_t *packed, const void *x, void *y, in
     if ((rc = check_dtype(dtype)) != TERNEL_TQ1_OK) return rc;
     if (uses_strip_gemv(M, batch_tile, k_split, rows, columns)) {
         // the same kernel as ternel_tq1_matmul; a split one meets its K
-        // chunks in the static scratch
+        // chunks in the static scratch's counter region
         StripGeometry geo;
         if ((rc = plan_strip(rows, columns, &geo)) != TERNEL_TQ1_OK) return rc;
         if ((rc = check_packed_pointer(packed)) != TERNEL_TQ1_OK) return rc;
         if (!x || !y) return fail(TERNEL_TQ1_EINVAL, "null pointer");
         hipStream_t s = static_cast<hipStream_t>(stream);
         void *ws = nullptr;
-        if (geo.Z > 1) {
-            if (strip_workspace_bytes(geo) - kPartialOffset > static_cast<size_t>(kNoAllocPartialBytes))
-                return fail(TERNEL_TQ1_EINVAL, "a split strip GEMV of %lld rows needs more partials than the %lld "
-                            "bytes of the static scratch", static_cast<long long>(rows),
-                            static_cast<long long>(kNoAllocPartialBytes));
-            if ((rc = noalloc_scratch(s, &ws)) != TERNEL_TQ1_OK) return rc;
-        }
+        if (geo.Z > 1 && (rc = noalloc_scratch(s, &ws)) != TERNEL_TQ1_OK) return rc;
         switch (dtype) {
             case TERNEL_TQ1_F16:
                 return launch_strip<_Float16>(packed, x, y, geo, s, false, ws);

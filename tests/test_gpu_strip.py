@@ -134,15 +134,18 @@ def test_fused_swiglu_form(dtype, rows) -> None:
     assert O.compare(got.cpu().numpy(), ref)["normalised_max_abs_error"] < 4 * TOLERANCE[dtype]
 
 
-# --- rows of 41 to 80 groups: the strip GEMV in Z = 2 K chunks, one workgroup
-# per (strip, chunk), S = CUs / 2 strips, met through two fp32 partials per
-# row added in chunk order by the chunk that arrives last.
+# --- rows of more than 40 groups: the strip GEMV in Z = ceil(G / 40) <= 4 K
+# chunks, one workgroup per (strip, chunk), S = CUs / Z strips; a row's chunk
+# partials meet in a fixed tree of exchange slots in the workspace's counter
+# region, (c0 + c1), ((c0 + c1) + c2) or ((c0 + c1) + (c2 + c3)).
 
 COUNTERS = 64 * 1024  # the workspace's counter region
 
 
 def takes_split_strip(rows: int, columns: int, chunks: int) -> bool:
-    return _lib.lib().ternel_tq1_matmul_workspace_bytes(1, rows, columns, 0, 0) == COUNTERS + chunks * rows * 4
+    # the (tile, group) kernel's split needs partials past the counter region
+    assert chunks == -(-columns // 128 // 40)
+    return _lib.lib().ternel_tq1_matmul_workspace_bytes(1, rows, columns, 0, 0) == COUNTERS
 
 
 def run_split(blocks: np.ndarray, x: torch.Tensor, chunks: int) -> torch.Tensor:
@@ -154,10 +157,12 @@ def run_split(blocks: np.ndarray, x: torch.Tensor, chunks: int) -> torch.Tensor:
 
 
 # (rows, columns, chunks): O 8192 -> 5120 (2 x 32 groups, 40-row strips);
-# out_proj 6144 -> 5120 (2 x 24); 41 groups (chunks of 21 and 20) over an odd
-# row count; 80 groups (2 x 40) over 18-row and over 64-row strips (three
-# items per wave).
-SPLIT_SHAPES = ((5120, 8192, 2), (5120, 6144, 2), (3001, 5248, 2), (2050, 10240, 2), (8192, 10240, 2))
+# down 17408 -> 5120 (4 x 34, 80 rows); out_proj 6144 -> 5120 (2 x 24); 41
+# groups (chunks of 21 and 20) over an odd row count; 80 groups over 64-row
+# strips (three items per wave); 96 groups (3 x 32, 85 strips); 112 groups
+# (38, 38, 36) over an odd row count; 160 groups (4 x 40) over 16-row strips.
+SPLIT_SHAPES = ((5120, 8192, 2), (5120, 17408, 4), (5120, 6144, 2), (3001, 5248, 2), (8192, 10240, 2),
+                (4096, 12288, 3), (3001, 14336, 3), (2050, 20480, 4))
 
 
 @pytest.mark.parametrize(("rows", "columns", "chunks"), SPLIT_SHAPES)
@@ -175,30 +180,34 @@ def test_split_strip_gemv_matches_the_oracle(rows, columns, chunks, dtype) -> No
 def test_split_strip_gemv_is_exact_on_integer_data() -> None:
     """Unit scales and +/-1 activations: every block sum, chunk partial and
     total is an exact integer, whatever the order."""
-    rows, columns = 5120, 10240
+    rows, columns = 5120, 17408
     groups = columns // 128
     rng = np.random.default_rng(41)
     scales = np.full(rows * groups, 1.0, dtype=np.float16).view(np.uint8).reshape(-1, 2)
     trits = rng.integers(0, 3, size=(rows * groups, 128), dtype=np.uint8)
     blocks = O.encode_tq1_blocks(scales, trits).reshape(rows, groups, 28)
     x = rng.choice((-1.0, 1.0), size=(1, columns)).astype(np.float32)
-    got = run_split(blocks, to_dev(x), 2).cpu().numpy()
+    got = run_split(blocks, to_dev(x), 4).cpu().numpy()
     np.testing.assert_array_equal(got, O.oracle_matmul(blocks, x, rows=rows, columns=columns))
 
 
 def test_split_strip_gemv_rearms_its_counters_and_repeats_bit_for_bit() -> None:
-    """Back-to-back calls of two shapes (different strip counts) on the
-    library's workspace: each call finds its counters at zero and leaves them
-    there, so every repeat is bit-identical."""
-    a = random_blocks(8192, 10240, seed=3)
+    """Back-to-back calls of shapes with different chunk counts and strip
+    counts on the library's workspace: each call finds its exchange slots
+    empty and leaves them so, and every repeat is bit-identical."""
+    a = random_blocks(5120, 17408, seed=3)
     b = random_blocks(5120, 8192, seed=4)
-    xa = to_dev(np.random.default_rng(3).normal(0.0, 1.0, size=(1, 10240)).astype(np.float16))
+    c = random_blocks(4096, 12288, seed=5)
+    xa = to_dev(np.random.default_rng(3).normal(0.0, 1.0, size=(1, 17408)).astype(np.float16))
     xb = to_dev(np.random.default_rng(4).normal(0.0, 1.0, size=(1, 8192)).astype(np.float16))
-    first_a = run_split(a, xa, 2).view(torch.int16).clone()
+    xc = to_dev(np.random.default_rng(5).normal(0.0, 1.0, size=(1, 12288)).astype(np.float16))
+    first_a = run_split(a, xa, 4).view(torch.int16).clone()
     first_b = run_split(b, xb, 2).view(torch.int16).clone()
+    first_c = run_split(c, xc, 3).view(torch.int16).clone()
     for _ in range(3):
-        assert torch.equal(run_split(a, xa, 2).view(torch.int16), first_a)
+        assert torch.equal(run_split(a, xa, 4).view(torch.int16), first_a)
         assert torch.equal(run_split(b, xb, 2).view(torch.int16), first_b)
+        assert torch.equal(run_split(c, xc, 3).view(torch.int16), first_c)
 
 
 def test_split_strip_gemv_unaligned_activations_give_the_same_result() -> None:

@@ -244,13 +244,16 @@ def test_workspace_queries() -> None:
     assert handle.ternel_tq1_swiglu_workspace_bytes(1, 12288, 5120, 0) == 0
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 24576, 5120, 0, 0) == 0
     assert handle.ternel_tq1_matmul_workspace_bytes(1, 24578, 5120, 0, 0) > 0  # 98-row strips: LUT23
-    # 41 to 80 groups: the strip GEMV in two K chunks, met through two fp32
-    # partials per row; past 80 groups LUT23
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 8192, 8192, 0, 0) == counters + 2 * 8192 * 4
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 10240, 0, 0) == counters + 2 * 5120 * 4
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 81 * 128, 0, 0) == (
-        handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 81 * 128, 1, 0))  # 81 groups: LUT23
-    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 17408, 0, 0) == counters + 17 * 5120 * 4
+    # more than 40 groups: the strip GEMV in Z = ceil(G / 40) <= 4 K chunks,
+    # whose row partials meet in Z - 1 exchange slots per row of the counter
+    # region (so at most 16368 slots); otherwise LUT23
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 8192, 8192, 0, 0) == counters
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 17408, 0, 0) == counters
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 17408, 1, 0) == counters + 17 * 5120 * 4
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 161 * 128, 0, 0) == (
+        handle.ternel_tq1_matmul_workspace_bytes(1, 5120, 161 * 128, 1, 0))  # 161 groups: LUT23
+    assert handle.ternel_tq1_matmul_workspace_bytes(1, 6144, 17408, 0, 0) == (
+        handle.ternel_tq1_matmul_workspace_bytes(1, 6144, 17408, 1, 0))  # 3 x 6144 slots: LUT23
     # the fused SwiGLU form is not split: LUT23 past 40 groups
     assert handle.ternel_tq1_swiglu_workspace_bytes(1, 8192, 8192, 0) == (
         handle.ternel_tq1_matmul_workspace_bytes(1, 8192, 8192, 1, 0))

@@ -59,9 +59,9 @@ CALL_PAIRS = (
     ((17408, 5120, 64, torch.float16, 0, 0), (4096, 4096, 1, torch.float16, 0, 0)),
     ((5120, 17408, 6, torch.bfloat16, 2, 0), (5120, 8192, 2, torch.bfloat16, 1, 8)),
     ((8192, 5120, 4, torch.float32, 4, 10), (640, 1024, 3, torch.float32, 1, 2)),
-    # one vector over 80 and then 64 groups: the strip GEMV in two K chunks,
-    # met in the scratch
-    ((8192, 10240, 1, torch.float16, 0, 0), (5120, 8192, 1, torch.float16, 0, 0)),
+    # one vector over 136 and then 64 groups: the strip GEMV in four, then
+    # two, K chunks, met in the scratch's counter region
+    ((5120, 17408, 1, torch.float16, 0, 0), (5120, 8192, 1, torch.float16, 0, 0)),
 )
 
 
