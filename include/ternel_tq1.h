@@ -153,10 +153,12 @@ int ternel_tq1_tiled_from_words(const uint32_t *packed, int64_t rows, int64_t co
  * gate/up 17408 x 5120 on 256 CUs)
  * runs a form that reduces every row inside one workgroup: no split, no
  * workspace, bit-identical from run to run, equal to the split result to
- * within fp32 reassociation of the per-group terms. A matrix of 41 to 80
- * groups per row whose strips (over half the CUs) stay within 96 rows (O
- * 8192 -> 5120) runs the same form in two K chunks per strip, met through
- * 64 KiB + 2 x rows x 4 bytes of workspace.
+ * within fp32 reassociation of the per-group terms. A matrix of 41 to 160
+ * groups per row whose strips (over CUs / Z) stay within 96 rows, with at
+ * most 16368 rows x (Z - 1) (down 17408 -> 5120, O 8192 -> 5120), runs the
+ * same form in Z = ceil(groups / 40) K chunks per strip, whose row partials
+ * meet in exchange slots in the 64 KiB counter region: its workspace is that
+ * region alone, left empty by every call.
  * ws: at least ternel_tq1_matmul_workspace_bytes(...) bytes (0 when the split
  * resolves to 1 or the unsplit form above runs; ws may then be NULL); see the
  * workspace contract above.
