@@ -466,9 +466,10 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic["bytes_per_launch"] if traffic else None,
             "kernel": f"{dom_name} GEMV K={dom_K} N={dom_N} ("
-                      + ("strip_gemv_kernel: every row reduced inside one workgroup, no split"
-                         if _lib.lib().ternel_tq1_matmul_workspace_bytes(1, dom_N, dom_K, 0, 0) == 0
-                         else "lut_gemv_kernel, fused ordered split-K") + ")",
+                      + {"strip": "strip_gemv_kernel: every row reduced inside one workgroup, no split",
+                         "lut23": "lut_gemv_kernel, fused ordered split-K"}.get(
+                          m1_form(_lib.lib(), dom_N, dom_K),
+                          "strip_gemv_kernel in K chunks meeting in exchange slots") + ")",
             "bytes_per_launch": dom_bytes,
             "mean_launch_us": round(graph_launch_ms * 1e3, 3),
             "timing": f"{args.steps} cold launches back to back in one HIP graph, events on the launch stream",
@@ -551,7 +552,8 @@ def main() -> int:
 
 PHASES = ("start", "activations arrived", "first words issued", "own tables written", "tables ready (barrier)",
           "blocks summed", "partial stored and acknowledged", "arrival counted", "fix-up done")
-# The strip GEMV's stamps (M=1 where a CU's strip is at most 96 rows and K <= 5120: gate/up, QKV).
+# The strip GEMV's stamps (M=1 where a CU's strip is at most 96 rows: gate/up, QKV, and down in
+# four K chunks, whose `done` includes the chunks' exchange).
 STRIP_PHASES = ("start", "activations arrived, first words issued", "tables ready", "all items summed", "done")
 # The wide form's stamps in the same slots (2-4 unused; 7 and 8 only where it reduces a shared tile).
 WIDE_PHASES = ("start", "first unit's operands in LDS", "-", "-", "-", "segment summed", "arrival counted",
@@ -590,7 +592,7 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
 
     for i, (name, K, N) in enumerate(C1_SHAPES):
         wide = batch > 1 and handle.ternel_tq1_linear_kernel(batch, N, K, 0) == 3  # TERNEL_TQ1_GEMM_WIDE
-        strip = batch == 1 and handle.ternel_tq1_matmul_workspace_bytes(1, N, K, 0, 0) == 0  # needs no workspace
+        strip = batch == 1 and m1_form(handle, N, K).startswith("strip")
         lut = handle.ternel_tq1_linear_kernel(batch, N, K, 0) == 100  # TERNEL_TQ1_KERNEL_LUT23
         names = WIDE_PHASES if wide else (STRIP_PHASES if strip else PHASES)
         lay = PackedTensorLayout.for_tensor(N, K)
@@ -637,7 +639,7 @@ def phase_profile(torch, dev, synthetic, pack_weights, tq1_matmul_words, tq1_lin
             continue
         print(json.dumps({
             "phase_profile": name, "K": K, "N": N, "M": batch, "waves_per_launch": len(phase_times["start"]) // 3,
-            "kernel": "wide_gemm_kernel" if wide else ("strip_gemv_kernel" if strip else
+            "kernel": "wide_gemm_kernel" if wide else (f"strip_gemv_kernel ({m1_form(handle, N, K)})" if strip else
                                                         ("lut_gemv_kernel" if lut else "direct_gemm_kernel")),
             "gemv_graph_us": round(graph_ms * 1e3, 3),
             "xcc_span_us": quantiles(spans),
