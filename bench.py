@@ -400,7 +400,8 @@ def main() -> int:
     c0_x = synthetic.device_activations(1, C0_K, seed=synthetic.SEED_BASE)
     config0 = {"workload": "BASELINE configs[0]: M=1, K=N=4096, fp16 activations, LUT23 GEMV "
                            "(the automatic configuration: the strip form)",
-               "packed_bytes": c0_bytes, "kernel": select_kernel(c0_layout, 1, torch.float16)}
+               "packed_bytes": c0_bytes, "kernel": select_kernel(c0_layout, 1, torch.float16),
+               "form": m1_form(_lib.lib(), C0_N, C0_K)}
     for label, copies in (("cold", c0_ring), ("warm", 1)):
         launches = max(c0_ring, 200)
         g = graph_of(lambda copies=copies: [tq1_matmul_words(c0_weights[s % copies], c0_x, layout=c0_layout,
