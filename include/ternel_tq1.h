@@ -45,9 +45,12 @@
  * workspace must not overlap in time (one workspace per stream). A kernel
  * whose bounded wait for another workgroup's published partial gives up
  * writes its tile as NaN (it sums nothing), sets the error word
- * (ternel_tq1_workspace_error) and may leave counters set; a launch that
- * finds the word set writes every tile needing the counters as NaN without
- * touching them. Zero the workspace again before reusing it.
+ * (ternel_tq1_workspace_error) and may leave counters set; a later launch of
+ * the wide form that finds the word set writes every tile needing the
+ * counters as NaN without touching them. The LUT23, direct-form and strip
+ * kernels do not read the word, and their results on a workspace whose
+ * counters were left set are not defined. Zero the workspace again before
+ * any further call on it.
  */
 #ifndef TERNEL_TQ1_H
 #define TERNEL_TQ1_H
